@@ -1,0 +1,197 @@
+/*
+ * inferrous_w8a8.h -- C ABI of the MI355X (gfx950) W8A8 linear-layer path.
+ *
+ * This is the drop-in boundary for the operator API that the reference's
+ * Qwen3 forward pass calls (bitemyapp/inferrous, crates/inferrous-qwen3/).
+ * There, ops are methods of the `LoadedModule` produced by
+ * `#[cuda_module] pub mod device` (src/kernels.rs:322-323) and created by
+ * `device::load(&ctx)` (src/gpu.rs:250).  Each entry point below names the
+ * reference kernel or runtime primitive it replaces (file:line relative to
+ * crates/inferrous-qwen3/).
+ *
+ * Conventions (mirroring src/gpu.rs and eng safety contract):
+ *  - All pointers are device pointers unless the name says host.  The caller
+ *    owns every buffer; ops allocate nothing, never synchronise, and run in
+ *    stream order on `stream` (a hipStream_t; NULL = the default stream), so
+ *    they are capturable into hip graphs.
+ *  - Shapes are explicit element counts: m activation rows (tokens), n output
+ *    channels, k = width (reduction length).  Weights are [n, k] int8 with k
+ *    contiguous (src/model.rs:23-28), activations [m, k], outputs [m, n].
+ *  - Every function returns an int status: 0 = ok, negative = invalid
+ *    argument detected on the host before any launch (see W8A8_E*), positive
+ *    = the hipError_t of a failed HIP call.  Nothing throws across the ABI.
+ *  - Launch geometry is chosen by the library; the reference's
+ *    LaunchConfig and L2-prefetch hint arguments have no counterpart.
+ */
+#ifndef INFERROUS_W8A8_H
+#define INFERROUS_W8A8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W8A8_ABI_VERSION 1
+
+/* status codes (negative: host-side validation) */
+#define W8A8_OK 0
+#define W8A8_ENULL (-1)      /* required pointer is NULL                 */
+#define W8A8_ESHAPE (-2)     /* inconsistent or unsupported dimensions   */
+#define W8A8_EALIGN (-3)     /* pointer alignment below the requirement  */
+#define W8A8_EINIT (-4)      /* w8a8_init not called / failed            */
+#define W8A8_EWORKSPACE (-5) /* workspace missing or too small           */
+#define W8A8_EARG (-6)       /* invalid enum or flag value               */
+#define W8A8_ENODEV (-7)     /* no usable gfx950 device                  */
+
+/* output element types for the dequant epilogue */
+#define W8A8_OUT_F32 0  /* f32 holding a BF16 value: the reference's buffers
+                           (src/kernels.rs:11-15 `bf` returns f32)           */
+#define W8A8_OUT_BF16 1 /* BF16 bits (uint16)                                 */
+#define W8A8_OUT_I32 2  /* raw exact INT32 accumulators, no epilogue          */
+
+/* kernel family selection for w8a8_linear_path (tests/bench); AUTO is what
+ * w8a8_linear uses */
+#define W8A8_PATH_AUTO 0
+#define W8A8_PATH_DOT4 1 /* v_dot4 GEMV, wave per row group           */
+#define W8A8_PATH_MFMA 2 /* LDS-staged v_mfma_i32_16x16x64_i8 GEMM    */
+
+/* ------------------------------------------------------------------ runtime
+ * Replaces cuda_core's CudaContext::new / new_stream / DeviceBuffer /
+ * PinnedHostBuffer / synchronize as used at src/gpu.rs:248-250,
+ * src/gpu.rs:59-61, src/gpu.rs:101, src/gpu.rs:147-181, src/gpu.rs:876,
+ * src/gpu.rs:910. */
+int w8a8_abi_version(void);
+const char *w8a8_status_string(int status);
+/* CudaContext::new(device) + device::load(&ctx) (src/gpu.rs:248-250):
+ * selects the device, checks it is gfx950, loads the kernels.  Idempotent. */
+int w8a8_init(int device);
+int w8a8_device_count(int *count);
+/* number of compute units and arch name of the current device */
+int w8a8_device_info(int *cu_count, char *arch_name, size_t arch_len);
+/* ctx.new_stream() (src/gpu.rs:249); *stream receives a hipStream_t */
+int w8a8_stream_create(void **stream);
+int w8a8_stream_destroy(void *stream);
+/* stream.synchronize() (src/gpu.rs:910) */
+int w8a8_stream_synchronize(void *stream);
+/* DeviceBuffer::zeroed (src/gpu.rs:101): zero-filled, 256-byte aligned */
+int w8a8_malloc(void **ptr, size_t bytes);
+int w8a8_free(void *ptr);
+/* PinnedHostBuffer (src/gpu.rs:147-181): page-locked host memory */
+int w8a8_host_malloc(void **ptr, size_t bytes);
+int w8a8_host_free(void *ptr);
+/* DeviceBuffer::from_host / copy_from_host / to_host_vec
+ * (src/gpu.rs:59-61, src/gpu.rs:876): stream-ordered copies */
+int w8a8_memcpy_htod(void *dst, const void *host_src, size_t bytes, void *stream);
+int w8a8_memcpy_dtoh(void *host_dst, const void *src, size_t bytes, void *stream);
+int w8a8_memcpy_dtod(void *dst, const void *src, size_t bytes, void *stream);
+/* zero a device range with a fill kernel (no hipMemsetAsync, graph-safe) */
+int w8a8_fill_zero(void *dst, size_t bytes, void *stream);
+/* events (timing); replaces the CUPTI/event timing of the reference tools */
+int w8a8_event_create(void **event);
+int w8a8_event_destroy(void *event);
+int w8a8_event_record(void *event, void *stream);
+int w8a8_event_synchronize(void *event);
+int w8a8_event_elapsed_ms(float *ms, void *start, void *stop);
+/* hip graph capture of a stream (src/graph.rs:330-458 equivalent, minimal) */
+int w8a8_graph_capture_begin(void *stream);
+int w8a8_graph_capture_end(void *stream, void **graph_exec);
+int w8a8_graph_launch(void *graph_exec, void *stream);
+int w8a8_graph_destroy(void *graph_exec);
+
+/* ------------------------------------------------------------------ ops */
+
+/* `rounding_probe` (src/kernels.rs:325-333): out[i] = round(input[i]) with
+ * clamp to [-127,127], round-half-even, NaN -> 0 (src/kernels.rs:24-34). */
+int w8a8_rounding_probe(void *stream, const float *input, size_t n, int8_t *out);
+
+/* `quantize` (src/kernels.rs:414-452): per row r of x[rows, width]:
+ *   m = max(1e-8, max_j |x_j|) ignoring NaN;  s = RN(m / 127);
+ *   q_j = round(RN(x_j / s));  scales[r] = s.
+ * If maxima_reset != NULL, also writes bits(1e-8f) to maxima_reset[r], the
+ * reset done by the quantize tail of `norm_quantize` (src/kernels.rs:566).
+ * x_bf16 variant: BF16 input bits, widened exactly (src/kernels.rs:16-19). */
+int w8a8_quantize(void *stream, const float *x, uint32_t width, size_t rows,
+                  int8_t *q, float *scales, uint32_t *maxima_reset);
+int w8a8_quantize_bf16(void *stream, const uint16_t *x, uint32_t width,
+                       size_t rows, int8_t *q, float *scales,
+                       uint32_t *maxima_reset);
+
+/* `quantize_with_max` (src/kernels.rs:453-475): as w8a8_quantize with
+ * m = from_bits(maxima[r]) published by the producer (src/kernels.rs:133-147). */
+int w8a8_quantize_with_max(void *stream, const float *x, uint32_t width,
+                           size_t rows, const uint32_t *maxima, int8_t *q,
+                           float *scales);
+
+/* `linear` (src/kernels.rs:807-845) for any m, and the M>1 GEMMs
+ * `linear_prefill` / `linear_splitk` / `linear_tiled` / `linear_large`
+ * (src/kernels.rs:846-1289) behind one entry, dispatched as
+ * `GpuModel::linear_quantized` does (src/gpu.rs:450-509):
+ *   acc[r][c] = sum_k q[r][k] * w[c][k]  (exact INT32)
+ *   out[r][c] = bf16(RN(RN(f32(acc) * asc[r]) * ws[c]))
+ * out_dtype: W8A8_OUT_F32 / _BF16 / _I32.  Requires k % 16 == 0 and
+ * 16-byte aligned q and w. */
+int w8a8_linear(void *stream, const int8_t *q, const float *asc, size_t m,
+                const int8_t *w, const float *ws, size_t n, uint32_t k,
+                void *out, int out_dtype);
+/* same with an explicit kernel family (W8A8_PATH_*) */
+int w8a8_linear_path(void *stream, const int8_t *q, const float *asc, size_t m,
+                     const int8_t *w, const float *ws, size_t n, uint32_t k,
+                     void *out, int out_dtype, int path);
+
+/* `linear_residual` (src/kernels.rs:577-618): the linear output plus
+ * combined = bf16(RN(residual + out)) (src/kernels.rs:615).  out and
+ * combined share out_dtype (F32 or BF16); residual is f32 [m, n]. */
+int w8a8_linear_residual(void *stream, const int8_t *q, const float *asc,
+                         size_t m, const int8_t *w, const float *ws, size_t n,
+                         uint32_t k, const float *residual, void *out,
+                         void *combined, int out_dtype);
+
+/* `linear_pair` (src/kernels.rs:696-735), `linear_triple`
+ * (src/kernels.rs:736-806) and the gate/up projections of `linear_swiglu`
+ * (src/kernels.rs:619-695): `count` (1..4) sibling projections that share
+ * the activations q/asc, in one launch.  w, ws, n, out are host arrays of
+ * length count; each projection writes its own out[i] [m, n[i]]. */
+int w8a8_linear_grouped(void *stream, const int8_t *q, const float *asc,
+                        size_t m, uint32_t k, int count,
+                        const int8_t *const *w, const float *const *ws,
+                        const size_t *n, void *const *out, int out_dtype);
+
+/* Greedy selection (`select_token`, src/kernels.rs:2191-2231): the largest
+ * value, lowest index on ties (-0 == +0); empty input or any non-finite
+ * value gives 0xFFFFFFFF.  Multi-workgroup: needs a device workspace of at
+ * least w8a8_select_workspace_bytes(n) bytes, zero-filled before its first
+ * use (w8a8_malloc does that); every call leaves it zeroed again.  Calls
+ * that share one workspace must not overlap. */
+size_t w8a8_select_workspace_bytes(size_t n);
+int w8a8_select_token(void *stream, const float *x, size_t n, uint32_t *token,
+                      void *workspace, size_t workspace_bytes);
+
+/* W8A8 lm_head with fused greedy selection: `linear` at m = 1 over n vocab
+ * rows followed by `select_token` over the BF16-rounded logits
+ * (src/gpu.rs:801-812 composition).  logits may be NULL; otherwise it
+ * receives the logits in logits_dtype (F32 or BF16).  Workspace as for
+ * w8a8_select_token, sized by w8a8_linear_argmax_workspace_bytes(n). */
+size_t w8a8_linear_argmax_workspace_bytes(size_t n);
+int w8a8_linear_argmax(void *stream, const int8_t *q, const float *asc,
+                       const int8_t *w, const float *ws, size_t n, uint32_t k,
+                       uint32_t *token, void *logits, int logits_dtype,
+                       void *workspace, size_t workspace_bytes);
+
+/* ------------------------------------------------------------------ synthetic
+ * Seeded generators for benches and tests (no reference counterpart; the
+ * reference loads exported bundles, src/model.rs:46-165).  Pure functions of
+ * (seed, stream, index), identical to the host definition used by the
+ * checker: element i of an int8 tensor takes 16 bits (i % 4) of
+ * hash(seed, stream, i / 4) mapped to [-127, 127]; an f32 tensor element is
+ * lo + RN(u * RN(hi - lo)) with u = (hash(seed, stream, i) >> 40) * 2^-24. */
+int w8a8_synth_i8(void *stream, int8_t *out, size_t n, uint64_t seed,
+                  uint64_t stream_id);
+int w8a8_synth_f32(void *stream, float *out, size_t n, uint64_t seed,
+                   uint64_t stream_id, float lo, float hi);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INFERROUS_W8A8_H */

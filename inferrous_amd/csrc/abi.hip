@@ -1,0 +1,487 @@
+// abi.hip -- the extern "C" boundary (include/inferrous_w8a8.h): runtime
+// primitives, host-side argument validation and kernel dispatch.
+//
+// Every entry validates its arguments on the host before any HIP call and
+// returns a negative W8A8_E* code on a violation, so misuse never reaches a
+// kernel.  HIP failures are returned as the positive hipError_t.  Ops only
+// launch kernels on the caller's stream: no allocation, no synchronisation,
+// no hipMemsetAsync (zeroing uses a fill kernel), hence graph-capturable.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/inferrous_w8a8.h"
+#include "internal.hpp"
+
+using namespace w8a8;
+
+namespace {
+
+std::mutex g_init_mu;
+std::atomic<uint64_t> g_ready_mask{0};  // devices that passed w8a8_init
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? W8A8_OK : (int)e; }
+
+inline bool ready() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  return (g_ready_mask.load(std::memory_order_acquire) >> dev) & 1u;
+}
+
+inline bool al(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+constexpr size_t kU32Max = 0xffffffffu;
+
+int out_align(int dtype) { return dtype == W8A8_OUT_BF16 ? 2 : 4; }
+
+bool valid_dtype(int dtype) {
+  return dtype == W8A8_OUT_F32 || dtype == W8A8_OUT_BF16 || dtype == W8A8_OUT_I32;
+}
+
+// Common checks of a single projection (q[m,k], asc[m], w[n,k], ws[n]).
+int check_linear(const int8_t* q, const float* asc, size_t m, const int8_t* w, const float* ws,
+                 size_t n, uint32_t k, const void* out, int out_dtype) {
+  if (!valid_dtype(out_dtype)) return W8A8_EARG;
+  if (m > kU32Max || n > kU32Max || k == 0 || k % 16 != 0) return W8A8_ESHAPE;
+  if (m > 0 && m * (size_t)k / k != m) return W8A8_ESHAPE;
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (!q || !asc || !w || !ws || !out) return W8A8_ENULL;
+  if (!al(q, 16) || !al(w, 16) || !al(asc, 4) || !al(ws, 4) || !al(out, out_align(out_dtype)))
+    return W8A8_EALIGN;
+  return W8A8_OK;
+}
+
+// dot4 GEMV for small m, MFMA beyond (see the crossover measurement).
+constexpr size_t kDot4MaxM = 2;
+
+int run_linear(hipStream_t st, const int8_t* q, const float* asc, size_t m, const int8_t* w,
+               const float* ws, size_t n, uint32_t k, void* out, int out_dtype, int path,
+               const float* residual, void* combined) {
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (path == W8A8_PATH_AUTO) path = m <= kDot4MaxM ? W8A8_PATH_DOT4 : W8A8_PATH_MFMA;
+  if (path == W8A8_PATH_DOT4) {
+    GemvArgs a{};
+    a.q = q;
+    a.asc = asc;
+    a.m = (uint32_t)m;
+    a.k = k;
+    a.count = 1;
+    a.w[0] = w;
+    a.ws[0] = ws;
+    a.n[0] = (uint32_t)n;
+    a.out[0] = out;
+    a.out_dtype = out_dtype;
+    a.residual = residual;
+    a.combined = combined;
+    return hip_status(launch_gemv(st, a));
+  }
+  GemmArgs g{};
+  g.q = q;
+  g.asc = asc;
+  g.m = (uint32_t)m;
+  g.w = w;
+  g.ws = ws;
+  g.n = (uint32_t)n;
+  g.k = k;
+  g.out = out;
+  g.out_dtype = out_dtype;
+  g.residual = residual;
+  g.combined = combined;
+  return hip_status(launch_gemm(st, g));
+}
+
+}  // namespace
+
+extern "C" {
+
+int w8a8_abi_version(void) { return W8A8_ABI_VERSION; }
+
+const char* w8a8_status_string(int status) {
+  switch (status) {
+    case W8A8_OK: return "ok";
+    case W8A8_ENULL: return "required pointer is NULL";
+    case W8A8_ESHAPE: return "inconsistent or unsupported dimensions";
+    case W8A8_EALIGN: return "pointer alignment below requirement";
+    case W8A8_EINIT: return "w8a8_init has not succeeded on the current device";
+    case W8A8_EWORKSPACE: return "workspace missing or too small";
+    case W8A8_EARG: return "invalid enum or flag value";
+    case W8A8_ENODEV: return "no usable gfx950 device";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "unknown status";
+}
+
+// ------------------------------------------------------------------ runtime
+int w8a8_device_count(int* count) {
+  if (!count) return W8A8_ENULL;
+  *count = 0;
+  int c = 0;
+  if (hipGetDeviceCount(&c) != hipSuccess) {
+    (void)hipGetLastError();
+    return W8A8_OK;
+  }
+  *count = c;
+  return W8A8_OK;
+}
+
+int w8a8_init(int device) {
+  if (device < 0 || device >= 64) return W8A8_EARG;
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  int c = 0;
+  if (hipGetDeviceCount(&c) != hipSuccess || device >= c) {
+    (void)hipGetLastError();
+    return W8A8_ENODEV;
+  }
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_status(e);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_status(e);
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return W8A8_ENODEV;
+  // force code-object load now (device::load) rather than at first launch
+  e = hipFree(nullptr);
+  if (e != hipSuccess) return hip_status(e);
+  g_ready_mask.fetch_or(1ull << device, std::memory_order_acq_rel);
+  return W8A8_OK;
+}
+
+int w8a8_device_info(int* cu_count, char* arch_name, size_t arch_len) {
+  if (!ready()) return W8A8_EINIT;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) return hip_status(e);
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  if (arch_name && arch_len) {
+    std::strncpy(arch_name, prop.gcnArchName, arch_len - 1);
+    arch_name[arch_len - 1] = 0;
+  }
+  return W8A8_OK;
+}
+
+int w8a8_stream_create(void** stream) {
+  if (!stream) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_status(e);
+  *stream = (void*)s;
+  return W8A8_OK;
+}
+
+int w8a8_stream_destroy(void* stream) {
+  if (!stream) return W8A8_ENULL;
+  return hip_status(hipStreamDestroy((hipStream_t)stream));
+}
+
+int w8a8_stream_synchronize(void* stream) {
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(hipStreamSynchronize((hipStream_t)stream));
+}
+
+int w8a8_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return W8A8_ENULL;
+  *ptr = nullptr;
+  if (!ready()) return W8A8_EINIT;
+  if (bytes == 0) bytes = 16;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return hip_status(e);
+  e = hipMemset(p, 0, bytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_status(e);
+  }
+  *ptr = p;
+  return W8A8_OK;
+}
+
+int w8a8_free(void* ptr) {
+  if (!ptr) return W8A8_OK;
+  return hip_status(hipFree(ptr));
+}
+
+int w8a8_host_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return W8A8_ENULL;
+  *ptr = nullptr;
+  if (!ready()) return W8A8_EINIT;
+  if (bytes == 0) bytes = 16;
+  return hip_status(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+}
+
+int w8a8_host_free(void* ptr) {
+  if (!ptr) return W8A8_OK;
+  return hip_status(hipHostFree(ptr));
+}
+
+int w8a8_memcpy_htod(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return W8A8_OK;
+  if (!dst || !src) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+}
+
+int w8a8_memcpy_dtoh(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return W8A8_OK;
+  if (!dst || !src) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+}
+
+int w8a8_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes == 0) return W8A8_OK;
+  if (!dst || !src) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+}
+
+int w8a8_fill_zero(void* dst, size_t bytes, void* stream) {
+  if (bytes == 0) return W8A8_OK;
+  if (!dst) return W8A8_ENULL;
+  if (!al(dst, 16)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_fill_zero((hipStream_t)stream, dst, bytes));
+}
+
+int w8a8_event_create(void** event) {
+  if (!event) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  hipEvent_t e = nullptr;
+  hipError_t r = hipEventCreate(&e);
+  if (r != hipSuccess) return hip_status(r);
+  *event = (void*)e;
+  return W8A8_OK;
+}
+
+int w8a8_event_destroy(void* event) {
+  if (!event) return W8A8_ENULL;
+  return hip_status(hipEventDestroy((hipEvent_t)event));
+}
+
+int w8a8_event_record(void* event, void* stream) {
+  if (!event) return W8A8_ENULL;
+  return hip_status(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+}
+
+int w8a8_event_synchronize(void* event) {
+  if (!event) return W8A8_ENULL;
+  return hip_status(hipEventSynchronize((hipEvent_t)event));
+}
+
+int w8a8_event_elapsed_ms(float* ms, void* start, void* stop) {
+  if (!ms || !start || !stop) return W8A8_ENULL;
+  return hip_status(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+}
+
+int w8a8_graph_capture_begin(void* stream) {
+  if (!stream) return W8A8_ENULL;  // the legacy default stream cannot be captured
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+}
+
+int w8a8_graph_capture_end(void* stream, void** graph_exec) {
+  if (!stream || !graph_exec) return W8A8_ENULL;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+  if (e != hipSuccess) return hip_status(e);
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_status(e);
+  *graph_exec = (void*)x;
+  return W8A8_OK;
+}
+
+int w8a8_graph_launch(void* graph_exec, void* stream) {
+  if (!graph_exec) return W8A8_ENULL;
+  return hip_status(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream));
+}
+
+int w8a8_graph_destroy(void* graph_exec) {
+  if (!graph_exec) return W8A8_ENULL;
+  return hip_status(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+}
+
+// ------------------------------------------------------------------ ops
+int w8a8_rounding_probe(void* stream, const float* input, size_t n, int8_t* out) {
+  if (n == 0) return W8A8_OK;
+  if (!input || !out) return W8A8_ENULL;
+  if (!al(input, 4)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_rounding_probe((hipStream_t)stream, input, n, out));
+}
+
+static int quantize_common(void* stream, const void* x, bool bf16, uint32_t width, size_t rows,
+                           int8_t* q, float* scales, uint32_t* maxima_reset) {
+  if (rows == 0) return W8A8_OK;
+  if (width == 0 || rows > 0x7fffffffu) return W8A8_ESHAPE;
+  if (rows * (size_t)width / width != rows) return W8A8_ESHAPE;
+  if (!x || !q || !scales) return W8A8_ENULL;
+  if (!al(x, bf16 ? 2 : 4) || !al(scales, 4) || !al(maxima_reset, 4)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_quantize((hipStream_t)stream, x, bf16, width, rows, q, scales, maxima_reset));
+}
+
+int w8a8_quantize(void* stream, const float* x, uint32_t width, size_t rows, int8_t* q,
+                  float* scales, uint32_t* maxima_reset) {
+  return quantize_common(stream, x, false, width, rows, q, scales, maxima_reset);
+}
+
+int w8a8_quantize_bf16(void* stream, const uint16_t* x, uint32_t width, size_t rows, int8_t* q,
+                       float* scales, uint32_t* maxima_reset) {
+  return quantize_common(stream, x, true, width, rows, q, scales, maxima_reset);
+}
+
+int w8a8_quantize_with_max(void* stream, const float* x, uint32_t width, size_t rows,
+                           const uint32_t* maxima, int8_t* q, float* scales) {
+  if (rows == 0) return W8A8_OK;
+  if (width == 0 || rows * (size_t)width / width != rows) return W8A8_ESHAPE;
+  if ((rows * (size_t)width) >> 40) return W8A8_ESHAPE;
+  if (!x || !maxima || !q || !scales) return W8A8_ENULL;
+  if (!al(x, 4) || !al(maxima, 4) || !al(scales, 4)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_quantize_with_max((hipStream_t)stream, x, width, rows, maxima, q, scales));
+}
+
+int w8a8_linear_path(void* stream, const int8_t* q, const float* asc, size_t m, const int8_t* w,
+                     const float* ws, size_t n, uint32_t k, void* out, int out_dtype, int path) {
+  if (path != W8A8_PATH_AUTO && path != W8A8_PATH_DOT4 && path != W8A8_PATH_MFMA) return W8A8_EARG;
+  int s = check_linear(q, asc, m, w, ws, n, k, out, out_dtype);
+  if (s != W8A8_OK || m == 0 || n == 0) return s;
+  if (!ready()) return W8A8_EINIT;
+  return run_linear((hipStream_t)stream, q, asc, m, w, ws, n, k, out, out_dtype, path, nullptr,
+                    nullptr);
+}
+
+int w8a8_linear(void* stream, const int8_t* q, const float* asc, size_t m, const int8_t* w,
+                const float* ws, size_t n, uint32_t k, void* out, int out_dtype) {
+  return w8a8_linear_path(stream, q, asc, m, w, ws, n, k, out, out_dtype, W8A8_PATH_AUTO);
+}
+
+int w8a8_linear_residual(void* stream, const int8_t* q, const float* asc, size_t m,
+                         const int8_t* w, const float* ws, size_t n, uint32_t k,
+                         const float* residual, void* out, void* combined, int out_dtype) {
+  if (out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  int s = check_linear(q, asc, m, w, ws, n, k, out, out_dtype);
+  if (s != W8A8_OK || m == 0 || n == 0) return s;
+  if (!residual || !combined) return W8A8_ENULL;
+  if (!al(residual, 4) || !al(combined, out_align(out_dtype))) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return run_linear((hipStream_t)stream, q, asc, m, w, ws, n, k, out, out_dtype, W8A8_PATH_AUTO,
+                    residual, combined);
+}
+
+int w8a8_linear_grouped(void* stream, const int8_t* q, const float* asc, size_t m, uint32_t k,
+                        int count, const int8_t* const* w, const float* const* ws, const size_t* n,
+                        void* const* out, int out_dtype) {
+  if (count < 1 || count > kMaxGroup) return W8A8_EARG;
+  if (!w || !ws || !n || !out) return W8A8_ENULL;
+  for (int i = 0; i < count; ++i) {
+    int s = check_linear(q, asc, m, w[i], ws[i], n[i], k, out[i], out_dtype);
+    if (s != W8A8_OK) return s;
+  }
+  if (m == 0) return W8A8_OK;
+  if (!ready()) return W8A8_EINIT;
+  hipStream_t st = (hipStream_t)stream;
+  if (m <= kDot4MaxM) {
+    GemvArgs a{};
+    a.q = q;
+    a.asc = asc;
+    a.m = (uint32_t)m;
+    a.k = k;
+    a.count = count;
+    for (int i = 0; i < count; ++i) {
+      a.w[i] = w[i];
+      a.ws[i] = ws[i];
+      a.n[i] = (uint32_t)n[i];
+      a.out[i] = out[i];
+    }
+    a.out_dtype = out_dtype;
+    return hip_status(launch_gemv(st, a));
+  }
+  for (int i = 0; i < count; ++i) {
+    int s = run_linear(st, q, asc, m, w[i], ws[i], n[i], k, out[i], out_dtype, W8A8_PATH_MFMA,
+                       nullptr, nullptr);
+    if (s != W8A8_OK) return s;
+  }
+  return W8A8_OK;
+}
+
+size_t w8a8_select_workspace_bytes(size_t n) { return 8 + 8 * (size_t)select_blocks(n); }
+
+int w8a8_select_token(void* stream, const float* x, size_t n, uint32_t* token, void* workspace,
+                      size_t workspace_bytes) {
+  if (n > kU32Max) return W8A8_ESHAPE;
+  if (!token) return W8A8_ENULL;
+  if (n > 0 && !x) return W8A8_ENULL;
+  if (!workspace || workspace_bytes < w8a8_select_workspace_bytes(n)) return W8A8_EWORKSPACE;
+  if (!al(x, 4) || !al(token, 4) || !al(workspace, 8)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  uint32_t* counter = (uint32_t*)workspace;
+  uint64_t* partials = (uint64_t*)workspace + 1;
+  return hip_status(launch_select((hipStream_t)stream, x, n, partials, counter, token));
+}
+
+size_t w8a8_linear_argmax_workspace_bytes(size_t n) {
+  // the k = 12288 configuration uses the most workgroups: an upper bound
+  return 8 + 8 * (size_t)gemv_argmax_blocks(n, 12288);
+}
+
+int w8a8_linear_argmax(void* stream, const int8_t* q, const float* asc, const int8_t* w,
+                       const float* ws, size_t n, uint32_t k, uint32_t* token, void* logits,
+                       int logits_dtype, void* workspace, size_t workspace_bytes) {
+  if (logits && logits_dtype != W8A8_OUT_F32 && logits_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  if (!token) return W8A8_ENULL;
+  if (n > 0) {
+    // validate as a 1-row projection; logits are optional
+    int s = check_linear(q, asc, 1, w, ws, n, k, logits ? logits : (void*)token,
+                         logits ? logits_dtype : W8A8_OUT_F32);
+    if (s != W8A8_OK) return s;
+  }
+  if (!al(token, 4)) return W8A8_EALIGN;
+  const size_t need = 8 + 8 * (size_t)gemv_argmax_blocks(n, k);
+  if (!workspace || workspace_bytes < need) return W8A8_EWORKSPACE;
+  if (!al(workspace, 8)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  GemvArgs a{};
+  a.q = q;
+  a.asc = asc;
+  a.m = 1;
+  a.k = k;
+  a.count = 1;
+  a.w[0] = w;
+  a.ws[0] = ws;
+  a.n[0] = (uint32_t)n;
+  a.out[0] = logits;
+  a.out_dtype = logits ? logits_dtype : W8A8_OUT_F32;
+  a.counter = (uint32_t*)workspace;
+  a.partials = (uint64_t*)workspace + 1;
+  a.token = token;
+  return hip_status(launch_gemv_argmax((hipStream_t)stream, a));
+}
+
+int w8a8_synth_i8(void* stream, int8_t* out, size_t n, uint64_t seed, uint64_t stream_id) {
+  if (n == 0) return W8A8_OK;
+  if (!out) return W8A8_ENULL;
+  if (!al(out, 16)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_synth_i8((hipStream_t)stream, out, n, seed, stream_id));
+}
+
+int w8a8_synth_f32(void* stream, float* out, size_t n, uint64_t seed, uint64_t stream_id, float lo,
+                   float hi) {
+  if (n == 0) return W8A8_OK;
+  if (!out) return W8A8_ENULL;
+  if (!al(out, 4)) return W8A8_EALIGN;
+  if (!(lo <= hi)) return W8A8_EARG;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_synth_f32((hipStream_t)stream, out, n, seed, stream_id, lo, hi));
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// device_common.hpp -- gfx950 device helpers shared by the W8A8 kernels.
+//
+// Exactness contract (restated from the reference, crates/inferrous-qwen3/):
+//   bf16_rne:  src/kernels.rs:11-15, bit formula including its wrap-around
+//   round_i8:  src/kernels.rs:24-34, clamp then round-half-even, NaN -> 0
+//   dequant:   src/kernels.rs:290, bf(RN(RN(f32(acc) * asc) * ws))
+// All HIP sources are built with -ffp-contract=off so no multiply is fused
+// with a neighbouring add, and f32 division / conversion stay IEEE RN.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w8a8 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr uint32_t kFloorBits = 0x322bcc77u;  // bits of 1e-8f
+
+__device__ __forceinline__ float bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ int8_t round_i8(float v) {
+  if (v != v) return 0;
+  v = __builtin_fminf(__builtin_fmaxf(v, -127.0f), 127.0f);
+  return (int8_t)(int)__builtin_rintf(v);  // v_rndne_f32: ties to even
+}
+
+// |x| as ordered bits with NaN mapped to 0 (f32::max ignores NaN,
+// src/kernels.rs:133-139); non-negative floats order like unsigned ints.
+__device__ __forceinline__ uint32_t abs_bits_no_nan(float x) {
+  uint32_t b = __float_as_uint(x) & 0x7fffffffu;
+  return b > 0x7f800000u ? 0u : b;
+}
+
+__device__ __forceinline__ float dequant(int32_t acc, float asc, float ws) {
+  float a = (float)acc;  // v_cvt_f32_i32, round to nearest even
+  float t = a * asc;
+  return bf16_rne(t * ws);
+}
+
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+__device__ __forceinline__ int dot16(v4i a, v4i b, int c) {
+  c = dot4(a.x, b.x, c);
+  c = dot4(a.y, b.y, c);
+  c = dot4(a.z, b.z, c);
+  c = dot4(a.w, b.w, c);
+  return c;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, kWave);
+    uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, kWave);
+    uint64_t w = ((uint64_t)hi << 32) | lo;
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// Greedy-selection key: orderable value in the high word, ~index in the low
+// word, so one unsigned max picks the largest value and, among equal values,
+// the lowest index (src/kernels.rs:2206-2209).  -0 is folded onto +0 so the
+// two tie (src/conformance.rs:685-686).  Any non-finite value yields the
+// all-ones key, which no finite value can produce (largest finite high word
+// is 0xff7fffff), and which maps to the u32::MAX sentinel.
+__device__ __forceinline__ uint64_t select_key(float v, uint32_t index) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7f800000u) == 0x7f800000u) return ~0ull;
+  if ((u & 0x7fffffffu) == 0u) u = 0u;
+  uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(~index);
+}
+
+__device__ __forceinline__ uint32_t key_to_token(uint64_t key) {
+  if (key == ~0ull || key == 0ull) return 0xffffffffu;
+  return ~(uint32_t)key;
+}
+
+// 16-byte loads.  Weights are streamed once per call: the non-temporal hint
+// keeps them from displacing the reused activations in L2 / MALL.
+__device__ __forceinline__ v4i load_nt16(const int8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+}
+__device__ __forceinline__ v4i load16(const int8_t* p) {
+  return *reinterpret_cast<const v4i*>(p);
+}
+
+}  // namespace w8a8

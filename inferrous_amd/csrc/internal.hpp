@@ -1,0 +1,66 @@
+// internal.hpp -- host-side launch interface between the C ABI layer
+// (abi.hip) and the kernel files.  Not installed; not part of the ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/inferrous_w8a8.h"
+
+namespace w8a8 {
+
+constexpr int kMaxGroup = 4;
+
+// One GEMV launch: up to kMaxGroup sibling projections sharing q/asc.
+struct GemvArgs {
+  const int8_t* q;
+  const float* asc;
+  uint32_t m, k;
+  int count;
+  const int8_t* w[kMaxGroup];
+  const float* ws[kMaxGroup];
+  uint32_t n[kMaxGroup];
+  uint32_t gbegin[kMaxGroup + 1];  // first row group of each projection (set by the launcher)
+  void* out[kMaxGroup];
+  int out_dtype;
+  const float* residual;  // EPI residual (count == 1)
+  void* combined;
+  uint64_t* partials;  // fused selection (count == 1, m == 1)
+  uint32_t* counter;
+  uint32_t* token;
+};
+
+struct GemmArgs {
+  const int8_t* q;
+  const float* asc;
+  uint32_t m;
+  const int8_t* w;
+  const float* ws;
+  uint32_t n, k;
+  void* out;
+  int out_dtype;
+  const float* residual;
+  void* combined;
+};
+
+hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t width, size_t rows,
+                           int8_t* q, float* scales, uint32_t* maxima_reset);
+hipError_t launch_quantize_with_max(hipStream_t st, const float* x, uint32_t width, size_t rows,
+                                    const uint32_t* maxima, int8_t* q, float* scales);
+hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8_t* out);
+
+hipError_t launch_gemv(hipStream_t st, GemvArgs& a);
+hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);
+uint32_t gemv_argmax_blocks(size_t n, uint32_t k);
+hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* partials,
+                         uint32_t* counter, uint32_t* token);
+uint32_t select_blocks(size_t n);
+
+hipError_t launch_gemm(hipStream_t st, const GemmArgs& a);
+
+hipError_t launch_synth_i8(hipStream_t st, int8_t* out, size_t n, uint64_t seed, uint64_t stream_id);
+hipError_t launch_synth_f32(hipStream_t st, float* out, size_t n, uint64_t seed, uint64_t stream_id,
+                            float lo, float hi);
+hipError_t launch_fill_zero(hipStream_t st, void* dst, size_t bytes);
+
+}  // namespace w8a8

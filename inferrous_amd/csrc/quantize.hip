@@ -1,0 +1,247 @@
+// quantize.hip -- dynamic per-token symmetric INT8 activation quantization.
+//
+// Reference semantics (crates/inferrous-qwen3/):
+//   quantize           src/kernels.rs:414-452
+//   quantize_with_max  src/kernels.rs:453-475
+//   norm_quantize tail src/kernels.rs:547-575 (maxima reset at :566)
+//   rounding_probe     src/kernels.rs:325-333
+//
+// MI355X design: one 256-thread workgroup (4 waves) per token row.  Each
+// thread loads its share of the row with 16-byte loads and keeps it in
+// registers (rows up to 16384 wide), so the row is read from HBM once: a
+// wave-level max over ordered |x| bits, a 4-entry LDS exchange, one RN
+// division for the scale, then RN divisions + clamp + round-half-even per
+// element and packed 4/8-byte stores of the int8 codes.
+#include "device_common.hpp"
+#include "internal.hpp"
+
+namespace w8a8 {
+
+constexpr int kQThreads = 256;
+constexpr int kQMaxVec = 16;  // f32: 16 x float4 per thread = 16384 wide
+
+__device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
+  m = wave_max_u32(m);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float s) {
+  uint32_t q0 = (uint8_t)round_i8(a / s), q1 = (uint8_t)round_i8(b / s);
+  uint32_t q2 = (uint8_t)round_i8(c / s), q3 = (uint8_t)round_i8(d / s);
+  return q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
+}
+
+// f32 rows, width % 4 == 0, 16-byte aligned rows.
+__global__ __launch_bounds__(kQThreads) void quantize_f32_vec(
+    const float* __restrict__ x, uint32_t width, int8_t* __restrict__ q,
+    float* __restrict__ scales, uint32_t* __restrict__ maxima_reset) {
+  __shared__ uint32_t red[4];
+  const size_t r = blockIdx.x;
+  const uint32_t nvec = width >> 2;
+  const v4f* row = reinterpret_cast<const v4f*>(x + r * width);
+  uint32_t* qrow = reinterpret_cast<uint32_t*>(q + r * width);
+  const uint32_t t = threadIdx.x;
+  const bool in_regs = nvec <= kQThreads * kQMaxVec;
+
+  v4f v[kQMaxVec];
+  uint32_t m = kFloorBits;
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kQMaxVec; ++i) {
+      const uint32_t j = t + i * kQThreads;
+      if (j < nvec) {
+        v[i] = row[j];
+        m = max(m, max(max(abs_bits_no_nan(v[i].x), abs_bits_no_nan(v[i].y)),
+                       max(abs_bits_no_nan(v[i].z), abs_bits_no_nan(v[i].w))));
+      }
+    }
+  } else {
+    for (uint32_t j = t; j < nvec; j += kQThreads) {
+      v4f a = row[j];
+      m = max(m, max(max(abs_bits_no_nan(a.x), abs_bits_no_nan(a.y)),
+                     max(abs_bits_no_nan(a.z), abs_bits_no_nan(a.w))));
+    }
+  }
+  m = block_max_256(m, red);
+  const float s = __uint_as_float(m) / 127.0f;
+  if (t == 0) {
+    scales[r] = s;
+    if (maxima_reset) maxima_reset[r] = kFloorBits;
+  }
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kQMaxVec; ++i) {
+      const uint32_t j = t + i * kQThreads;
+      if (j < nvec) qrow[j] = pack4(v[i].x, v[i].y, v[i].z, v[i].w, s);
+    }
+  } else {
+    for (uint32_t j = t; j < nvec; j += kQThreads) {
+      v4f a = row[j];
+      qrow[j] = pack4(a.x, a.y, a.z, a.w, s);
+    }
+  }
+}
+
+__device__ __forceinline__ float widen(uint32_t h) { return __uint_as_float(h << 16); }
+
+// BF16 rows, width % 8 == 0, 16-byte aligned rows: 8 values per 16 bytes.
+__global__ __launch_bounds__(kQThreads) void quantize_bf16_vec(
+    const uint16_t* __restrict__ x, uint32_t width, int8_t* __restrict__ q,
+    float* __restrict__ scales, uint32_t* __restrict__ maxima_reset) {
+  __shared__ uint32_t red[4];
+  constexpr int kMax = kQMaxVec / 2;
+  const size_t r = blockIdx.x;
+  const uint32_t nvec = width >> 3;
+  const v4i* row = reinterpret_cast<const v4i*>(x + r * width);
+  v2i* qrow = reinterpret_cast<v2i*>(q + r * width);
+  const uint32_t t = threadIdx.x;
+  const bool in_regs = nvec <= kQThreads * kMax;
+
+  v4i v[kMax];
+  uint32_t m = kFloorBits;
+  auto absmax8 = [](v4i a) {
+    uint32_t mm = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t w = (uint32_t)a[e];
+      mm = max(mm, max(abs_bits_no_nan(widen(w & 0xffffu)), abs_bits_no_nan(widen(w >> 16))));
+    }
+    return mm;
+  };
+  auto quant8 = [](v4i a, float s) {
+    v2i o;
+    o.x = (int)pack4(widen((uint32_t)a.x & 0xffffu), widen((uint32_t)a.x >> 16),
+                     widen((uint32_t)a.y & 0xffffu), widen((uint32_t)a.y >> 16), s);
+    o.y = (int)pack4(widen((uint32_t)a.z & 0xffffu), widen((uint32_t)a.z >> 16),
+                     widen((uint32_t)a.w & 0xffffu), widen((uint32_t)a.w >> 16), s);
+    return o;
+  };
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kMax; ++i) {
+      const uint32_t j = t + i * kQThreads;
+      if (j < nvec) {
+        v[i] = row[j];
+        m = max(m, absmax8(v[i]));
+      }
+    }
+  } else {
+    for (uint32_t j = t; j < nvec; j += kQThreads) m = max(m, absmax8(row[j]));
+  }
+  m = block_max_256(m, red);
+  const float s = __uint_as_float(m) / 127.0f;
+  if (t == 0) {
+    scales[r] = s;
+    if (maxima_reset) maxima_reset[r] = kFloorBits;
+  }
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kMax; ++i) {
+      const uint32_t j = t + i * kQThreads;
+      if (j < nvec) qrow[j] = quant8(v[i], s);
+    }
+  } else {
+    for (uint32_t j = t; j < nvec; j += kQThreads) qrow[j] = quant8(row[j], s);
+  }
+}
+
+// Any width / alignment: scalar two-pass fallback (second pass hits L2).
+template <bool BF16>
+__global__ __launch_bounds__(kQThreads) void quantize_scalar(
+    const void* __restrict__ xv, uint32_t width, int8_t* __restrict__ q,
+    float* __restrict__ scales, uint32_t* __restrict__ maxima_reset) {
+  __shared__ uint32_t red[4];
+  const size_t r = blockIdx.x;
+  auto load = [&](uint32_t j) -> float {
+    if (BF16) return widen(reinterpret_cast<const uint16_t*>(xv)[r * width + j]);
+    return reinterpret_cast<const float*>(xv)[r * width + j];
+  };
+  uint32_t m = kFloorBits;
+  for (uint32_t j = threadIdx.x; j < width; j += kQThreads) m = max(m, abs_bits_no_nan(load(j)));
+  m = block_max_256(m, red);
+  const float s = __uint_as_float(m) / 127.0f;
+  if (threadIdx.x == 0) {
+    scales[r] = s;
+    if (maxima_reset) maxima_reset[r] = kFloorBits;
+  }
+  for (uint32_t j = threadIdx.x; j < width; j += kQThreads) q[r * width + j] = round_i8(load(j) / s);
+}
+
+// quantize_with_max: elementwise, 4 per thread when width % 4 == 0.
+__global__ __launch_bounds__(256) void quantize_with_max_vec(
+    const float* __restrict__ x, uint32_t width, size_t total_vec,
+    const uint32_t* __restrict__ maxima, int8_t* __restrict__ q, float* __restrict__ scales) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total_vec) return;
+  const size_t e = i * 4;
+  const size_t r = e / width;
+  const float s = __uint_as_float(maxima[r]) / 127.0f;
+  v4f a = reinterpret_cast<const v4f*>(x)[i];
+  reinterpret_cast<uint32_t*>(q)[i] = pack4(a.x, a.y, a.z, a.w, s);
+  if (e % width == 0) scales[r] = s;
+}
+
+__global__ __launch_bounds__(256) void quantize_with_max_scalar(
+    const float* __restrict__ x, uint32_t width, size_t total,
+    const uint32_t* __restrict__ maxima, int8_t* __restrict__ q, float* __restrict__ scales) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const size_t r = i / width;
+  const float s = __uint_as_float(maxima[r]) / 127.0f;
+  q[i] = round_i8(x[i] / s);
+  if (i % width == 0) scales[r] = s;
+}
+
+__global__ __launch_bounds__(256) void rounding_probe_kernel(const float* __restrict__ in, size_t n,
+                                                              int8_t* __restrict__ out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = round_i8(in[i]);
+}
+
+// ------------------------------------------------------------------ launchers
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t width, size_t rows,
+                           int8_t* q, float* scales, uint32_t* maxima_reset) {
+  if (rows == 0 || width == 0) return hipSuccess;
+  dim3 grid((unsigned)rows), block(kQThreads);
+  if (!bf16 && width % 4 == 0 && aligned16(x) && ((uintptr_t)q & 3u) == 0)
+    hipLaunchKernelGGL(quantize_f32_vec, grid, block, 0, st, (const float*)x, width, q, scales,
+                       maxima_reset);
+  else if (bf16 && width % 8 == 0 && aligned16(x) && ((uintptr_t)q & 7u) == 0)
+    hipLaunchKernelGGL(quantize_bf16_vec, grid, block, 0, st, (const uint16_t*)x, width, q, scales,
+                       maxima_reset);
+  else if (bf16)
+    hipLaunchKernelGGL(quantize_scalar<true>, grid, block, 0, st, x, width, q, scales, maxima_reset);
+  else
+    hipLaunchKernelGGL(quantize_scalar<false>, grid, block, 0, st, x, width, q, scales,
+                       maxima_reset);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_with_max(hipStream_t st, const float* x, uint32_t width, size_t rows,
+                                    const uint32_t* maxima, int8_t* q, float* scales) {
+  const size_t total = rows * (size_t)width;
+  if (total == 0) return hipSuccess;
+  if (width % 4 == 0 && aligned16(x) && ((uintptr_t)q & 3u) == 0) {
+    const size_t nv = total / 4;
+    hipLaunchKernelGGL(quantize_with_max_vec, dim3((unsigned)((nv + 255) / 256)), dim3(256), 0, st,
+                       x, width, nv, maxima, q, scales);
+  } else {
+    hipLaunchKernelGGL(quantize_with_max_scalar, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       0, st, x, width, total, maxima, q, scales);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8_t* out) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(rounding_probe_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     in, n, out);
+  return hipGetLastError();
+}
+
+}  // namespace w8a8

@@ -1,0 +1,98 @@
+/*
+ * w8a8_oracle.h -- CPU restatement of the reference's W8A8 linear-layer
+ * arithmetic.  TEST INFRASTRUCTURE ONLY: this library is the checker used by
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.  The
+ * product path (inferrous_amd/) never links, loads or calls it.
+ *
+ * Every function cites the reference file:line whose semantics it restates.
+ * Paths are relative to crates/inferrous-qwen3/ in bitemyapp/inferrous.
+ */
+#ifndef W8A8_ORACLE_H
+#define W8A8_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* src/kernels.rs:11-15 `bf`: f32 -> BF16 round-to-nearest-even kept in f32,
+ * computed on the bit pattern exactly as the reference does (including its
+ * behaviour on NaN/overflow encodings). */
+float orc_bf16_rne(float x);
+/* Same value as BF16 bits (high half of orc_bf16_rne). */
+uint16_t orc_bf16_bits(float x);
+
+/* src/kernels.rs:24-34 `round`: clamp(x,-127,127), round half to even,
+ * NaN -> 0, low byte as i8. */
+int8_t orc_round_i8(float x);
+void orc_round_many(const float *x, size_t n, int8_t *out);
+
+/* Row absmax as the reference's quantizers see it (src/kernels.rs:433-438,
+ * f32::max ignores NaN, floor 1e-8), returned as f32 bits.  Equals the
+ * producer-published maximum of src/kernels.rs:133-147 seeded with
+ * bits(1e-8) (src/kernels.rs:566). */
+uint32_t orc_absmax_bits(const float *x, size_t n);
+
+/* src/kernels.rs:414-452 `quantize` per row: s = RN(m/127),
+ * q_j = round(RN(x_j/s)).  rows x width, row-major. */
+void orc_quantize_rows(const float *x, size_t rows, size_t width, int8_t *q,
+                       float *scales);
+/* Same with BF16 input bits (values widened exactly to f32 first,
+ * src/kernels.rs:16-19 `widen`). */
+void orc_quantize_rows_bf16(const uint16_t *x, size_t rows, size_t width,
+                            int8_t *q, float *scales);
+/* src/kernels.rs:453-475 `quantize_with_max`: m = from_bits(maxima[r]). */
+void orc_quantize_rows_with_max(const float *x, size_t rows, size_t width,
+                                const uint32_t *maxima, int8_t *q,
+                                float *scales);
+
+/* Exact INT32 accumulators acc[r][c] = sum_k q[r][k] * w[c][k]
+ * (src/kernels.rs:268-291, src/kernels.rs:807-845; weights [N,K] with K
+ * contiguous per src/model.rs:23-28).  nthreads<=0 -> single thread. */
+void orc_linear_i32(const int8_t *q, size_t m, const int8_t *w, size_t n,
+                    size_t k, int32_t *acc, int nthreads);
+
+/* Epilogue of src/kernels.rs:289-290 / :839-843 / :918-930:
+ * out = bf(RN(RN(f32(acc) * asc[r]) * ws[c])).  out_f32 and/or out_bf16
+ * may be NULL. */
+void orc_epilogue(const int32_t *acc, const float *asc, size_t m,
+                  const float *ws, size_t n, float *out_f32,
+                  uint16_t *out_bf16);
+
+/* Full linear (i32 GEMM + epilogue). Any output pointer may be NULL. */
+void orc_linear(const int8_t *q, const float *asc, size_t m, const int8_t *w,
+                const float *ws, size_t n, size_t k, int32_t *acc_out,
+                float *out_f32, uint16_t *out_bf16, int nthreads);
+
+/* src/kernels.rs:615 / :2163-2170: combined = bf(RN(residual + out)). */
+void orc_residual(const float *residual, const float *out, size_t n,
+                  float *combined);
+
+/* src/kernels.rs:2191-2231 `select_token` (equal to src/model.rs:206-218
+ * `argmax` when that returns Ok): largest value, lowest index on ties,
+ * -0 == +0; empty input or any non-finite value -> 0xFFFFFFFF. */
+uint32_t orc_argmax(const float *x, size_t n);
+
+/* lm_head composition (linear at N=vocab, then select_token over the BF16
+ * logits). logits_f32 may be NULL. */
+uint32_t orc_linear_argmax(const int8_t *q, const float *asc, const int8_t *w,
+                           const float *ws, size_t n, size_t k,
+                           float *logits_f32, int nthreads);
+
+/* ---- Seeded synthetic generators (shared definition with the device
+ * generator in inferrous_amd/csrc/synth.hip).  Pure functions of
+ * (seed, stream, index); used to regenerate spot rows on the host. ---- */
+uint64_t orc_mix64(uint64_t x);
+uint64_t orc_synth_hash(uint64_t seed, uint64_t stream, uint64_t index);
+/* int8 uniform over the 255 values [-127,127]. */
+void orc_synth_i8(uint64_t seed, uint64_t stream, uint64_t first, size_t n,
+                  int8_t *out);
+/* f32 uniform in [lo, hi): lo + u*(hi-lo), u = (h>>40)*2^-24, two RN ops. */
+void orc_synth_f32(uint64_t seed, uint64_t stream, uint64_t first, size_t n,
+                   float lo, float hi, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,105 @@
+"""Shared pytest configuration.
+
+Markers:
+  gpu -- needs an MI355X (gfx950) and the built HIP library; run with -m gpu.
+
+Everything else runs on the CPU: oracle pinning against golden vectors and
+closed forms, C-ABI load/export checks and host-side argument validation.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: requires an MI355X GPU and the built HIP library")
+
+
+class Fixtures:
+    """Reader for the reference-format operator fixture manifest."""
+
+    def __init__(self, root: Path):
+        self.root = root
+        self.manifest = json.loads((root / "manifest.json").read_text())
+
+    def cases(self, op: str):
+        return [c for c in self.manifest["cases"] if c["op"] == op]
+
+    def tensor(self, case: dict, key: str) -> np.ndarray:
+        meta = case["tensors"][key]
+        raw = (self.root / meta["file"]).read_bytes()
+        assert hashlib.sha256(raw).hexdigest() == meta["sha256"], f"fixture hash: {key}"
+        return np.frombuffer(raw, dtype=np.dtype(meta["dtype"])).reshape(meta["shape"]).copy()
+
+
+@pytest.fixture(scope="session")
+def fixtures() -> Fixtures:
+    return Fixtures(GOLDEN / "operator")
+
+
+def rounding_probe_inputs() -> np.ndarray:
+    """The deterministic input set of src/conformance.rs:841-856 (1,328,443 f32):
+    every BF16 encoding, a dense signed grid in 1/1024 steps over [-128, 128],
+    the +-1-ulp neighbours of every half-integer tie in (-127, 127), and one
+    million hashed f32 bit patterns (x * 2654435761 mod 2^32)."""
+    parts = [(np.arange(65536, dtype=np.uint32) << 16).view(np.float32)]
+    parts.append((np.arange(-131072, 131073, dtype=np.float64) / 1024.0).astype(np.float32))
+    ties = []
+    for i in range(-127, 127):
+        b = int(np.float32(i + 0.5).view(np.uint32))
+        ties += [b - 1, b, b + 1]
+    parts.append(np.array(ties, dtype=np.uint32).view(np.float32))
+    x = np.arange(1_000_000, dtype=np.uint64)
+    parts.append(((x * 2654435761) & 0xFFFFFFFF).astype(np.uint32).view(np.float32))
+    return np.concatenate(parts)
+
+
+def rounding_expected(x: np.ndarray) -> np.ndarray:
+    """Closed form of src/conformance.rs:857-860: f64 clamp to [-127, 127],
+    round half to even, NaN -> 0 (Rust's saturating `as i8`)."""
+    d = x.astype(np.float64)
+    nan = np.isnan(d)
+    d = np.clip(np.where(nan, 0.0, d), -127.0, 127.0)
+    return np.rint(d).astype(np.int8)
+
+
+def argmax_cases() -> list[np.ndarray]:
+    """src/conformance.rs:684-698: six hand cases plus, for each length in
+    {31, 32, 33, 1023, 1024, 1025, 151936}, i % 97 with f32::MAX at the end,
+    then additionally at index 7 (repeated maximum, lowest index wins)."""
+    f = np.float32
+    big = np.finfo(np.float32).max
+    cases = [np.array(v, dtype=f) for v in (
+        [0.0, -0.0], [-0.0, 0.0], [np.finfo(np.float32).min], [np.nan],
+        [0.0, np.inf], [-np.inf, 0.0])]
+    for n in (31, 32, 33, 1023, 1024, 1025, 151936):
+        x = (np.arange(n) % 97).astype(f)
+        x[n - 1] = big
+        cases.append(x.copy())
+        x[7] = big
+        cases.append(x)
+    return cases
+
+
+def argmax_expected(x: np.ndarray) -> int:
+    """src/model.rs:206-218 `argmax`, Err mapped to the GPU sentinel u32::MAX
+    (src/conformance.rs:707): strict '>' ascending scan."""
+    if x.size == 0 or not np.all(np.isfinite(x)):
+        return 0xFFFFFFFF
+    best = 0
+    for i in range(1, x.size):
+        if x[i] > x[best]:
+            best = i
+    return best

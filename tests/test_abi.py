@@ -1,0 +1,135 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects malformed arguments on the host (negative status
+codes) before any HIP call.  With no device present, well-formed calls stop at
+the init check (W8A8_EINIT) -- never at a launch."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from inferrous_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "inferrous_w8a8.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(w8a8_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declarations_match_binding():
+    assert declared_symbols() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = declared_symbols() - exported
+    assert not missing, missing
+    L = _lib.lib()
+    for name in declared_symbols():
+        assert getattr(L, name) is not None
+
+
+def test_library_targets_gfx950_only():
+    """The offload bundle ids embedded in our own build name gfx950 only."""
+    blob = _lib.LIB_PATH.read_bytes()
+    arches = set(re.findall(rb"amdgcn-amd-amdhsa--(gfx[0-9a-z]+)", blob))
+    assert arches == {b"gfx950"}, arches
+
+
+def test_abi_version_and_status_strings():
+    L = _lib.lib()
+    assert L.w8a8_abi_version() == 1
+    for code in (_lib.OK, _lib.ENULL, _lib.ESHAPE, _lib.EALIGN, _lib.EINIT, _lib.EWORKSPACE,
+                 _lib.EARG, _lib.ENODEV):
+        assert L.w8a8_status_string(code)
+
+
+A = 0x10000  # fake, aligned device addresses: validation never dereferences them
+
+
+def lin(**kw):
+    args = dict(stream=None, q=A, asc=A, m=1, w=A, ws=A, n=33, k=4096, out=A, dtype=_lib.OUT_F32,
+                path=_lib.PATH_AUTO)
+    args.update(kw)
+    return _lib.lib().w8a8_linear_path(args["stream"], args["q"], args["asc"], args["m"], args["w"],
+                                       args["ws"], args["n"], args["k"], args["out"], args["dtype"],
+                                       args["path"])
+
+
+def no_device_status():
+    c = ctypes.c_int()
+    _lib.lib().w8a8_device_count(ctypes.byref(c))
+    return c.value
+
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_linear_validation_precedes_device():
+    assert lin() == _lib.EINIT                       # well formed: stops at init
+    assert lin(k=4095) == _lib.ESHAPE                # k % 16
+    assert lin(k=0) == _lib.ESHAPE
+    assert lin(m=1 << 33) == _lib.ESHAPE
+    assert lin(q=None) == _lib.ENULL
+    assert lin(ws=None) == _lib.ENULL
+    assert lin(q=A + 8) == _lib.EALIGN               # 16-byte operand alignment
+    assert lin(w=A + 4) == _lib.EALIGN
+    assert lin(out=A + 2) == _lib.EALIGN             # f32 output needs 4 bytes
+    assert lin(out=A + 2, dtype=_lib.OUT_BF16) == _lib.EINIT
+    assert lin(dtype=7) == _lib.EARG
+    assert lin(path=9) == _lib.EARG
+    assert lin(m=0) == _lib.OK and lin(n=0) == _lib.OK  # empty problems are no-ops
+
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_other_ops_validation():
+    L = _lib.lib()
+    assert L.w8a8_quantize(None, A, 4096, 1, A, A, None) == _lib.EINIT
+    assert L.w8a8_quantize(None, None, 4096, 1, A, A, None) == _lib.ENULL
+    assert L.w8a8_quantize(None, A, 0, 1, A, A, None) == _lib.ESHAPE
+    assert L.w8a8_quantize(None, A + 2, 4096, 1, A, A, None) == _lib.EALIGN
+    assert L.w8a8_quantize_bf16(None, A + 2, 4096, 1, A, A, None) == _lib.EINIT
+    assert L.w8a8_quantize_with_max(None, A, 4096, 1, None, A, A) == _lib.ENULL
+    assert L.w8a8_rounding_probe(None, A, 10, None) == _lib.ENULL
+    # residual needs both extra buffers and a float epilogue
+    assert L.w8a8_linear_residual(None, A, A, 1, A, A, 8, 4096, None, A, A, _lib.OUT_F32) == _lib.ENULL
+    assert L.w8a8_linear_residual(None, A, A, 1, A, A, 8, 4096, A, A, A, _lib.OUT_I32) == _lib.EARG
+    # grouped: 1..4 projections
+    W = (ctypes.c_void_p * 4)(A, A, A, A)
+    N = (ctypes.c_size_t * 4)(8, 8, 8, 8)
+    assert L.w8a8_linear_grouped(None, A, A, 1, 4096, 0, W, W, N, W, 0) == _lib.EARG
+    assert L.w8a8_linear_grouped(None, A, A, 1, 4096, 5, W, W, N, W, 0) == _lib.EARG
+    assert L.w8a8_linear_grouped(None, A, A, 1, 4096, 3, W, W, N, W, 0) == _lib.EINIT
+    # selection workspaces
+    need = L.w8a8_select_workspace_bytes(151936)
+    assert need >= 16
+    assert L.w8a8_select_token(None, A, 151936, A, A, need - 8) == _lib.EWORKSPACE
+    assert L.w8a8_select_token(None, A, 151936, A, None, need) == _lib.EWORKSPACE
+    assert L.w8a8_select_token(None, A, 151936, A, A, need) == _lib.EINIT
+    need = L.w8a8_linear_argmax_workspace_bytes(151936)
+    assert L.w8a8_linear_argmax(None, A, A, A, A, 151936, 4096, A, None, 0, A, need) == _lib.EINIT
+    assert L.w8a8_linear_argmax(None, A, A, A, A, 151936, 4096, A, None, 0, A, 8) == _lib.EWORKSPACE
+    assert L.w8a8_linear_argmax(None, A, A, A, A, 151936, 4096, None, None, 0, A, need) == _lib.ENULL
+    assert L.w8a8_linear_argmax(None, A, A, A, A, 151936, 4096, A, A, _lib.OUT_I32, A, need) == _lib.EARG
+    assert L.w8a8_synth_i8(None, A + 1, 100, 1, 2) == _lib.EALIGN
+    assert L.w8a8_synth_f32(None, A, 100, 1, 2, 2.0, 1.0) == _lib.EARG
+    # runtime primitives refuse to run before init
+    p = ctypes.c_void_p()
+    assert L.w8a8_malloc(ctypes.byref(p), 64) == _lib.EINIT
+    assert L.w8a8_stream_create(ctypes.byref(p)) == _lib.EINIT
+    assert L.w8a8_init(-1) == _lib.EARG
+    assert L.w8a8_init(0) == _lib.ENODEV
+
+
+def test_module_requires_library_not_oracle():
+    """The product package never imports the oracle."""
+    for py in (ROOT / "inferrous_amd").rglob("*.py"):
+        text = py.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, py

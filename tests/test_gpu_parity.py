@@ -1,0 +1,336 @@
+"""GPU parity: every op through the C ABI against the CPU oracle, the committed
+fixtures and the reference's own test vectors.  Bit-exact for int8 codes,
+scales, i32 accumulators, BF16 outputs and token ids (the north-star bar is
+1 BF16 ulp; nothing here needs it).
+
+Layout follows crates/inferrous-qwen3/src/conformance.rs: each op is called
+as ``module.op(stream, cfg, ...)`` on the same inputs as the reference's
+tests, and each kernel family is forced on every fixture.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import argmax_cases, argmax_expected, rounding_expected, rounding_probe_inputs
+from inferrous_amd import (CudaContext, DeviceBuffer, Event, Graph, W8A8Error, cfg, load, rows)
+from inferrous_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def env():
+    ctx = CudaContext(0)
+    stream = ctx.new_stream()
+    return ctx, load(ctx), stream
+
+
+def dev(stream, a):
+    return DeviceBuffer.from_host(stream, np.ascontiguousarray(a))
+
+
+# ------------------------------------------------------------------ rounding
+def test_rounding_probe_reference_set(env):
+    ctx, mod, s = env
+    x = rounding_probe_inputs()
+    out = DeviceBuffer.zeroed(s, x.size, np.int8)
+    mod.rounding_probe(s, cfg(x.size), dev(s, x), out)
+    got = out.to_host_vec(s)
+    want = rounding_expected(x)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"first mismatch input bits {x[bad[0]].view(np.uint32):08x}"
+
+
+# ------------------------------------------------------------------ quantize
+def test_quantize_fixtures(env, fixtures):
+    ctx, mod, s = env
+    for c in fixtures.cases("quantize"):
+        w = c["width"]
+        x = fixtures.tensor(c, "x").reshape(-1)
+        q = DeviceBuffer.zeroed(s, x.size, np.int8)
+        sc = DeviceBuffer.zeroed(s, x.size // w, np.float32)
+        maxima = dev(s, np.full(x.size // w, 7, np.uint32))
+        mod.quantize(s, rows(x.size // w, 1024), dev(s, x), w, q, sc, maxima_reset=maxima)
+        assert np.array_equal(q.to_host_vec(s), fixtures.tensor(c, "q").reshape(-1)), c["name"]
+        assert np.array_equal(bits(sc.to_host_vec(s)), bits(fixtures.tensor(c, "scale").reshape(-1)))
+        assert np.all(maxima.to_host_vec(s) == np.float32(1e-8).view(np.uint32))
+        # producer-max path reproduces the scan (src/conformance.rs:129-152)
+        mx = np.array([oracle.absmax_bits(r) for r in x.reshape(-1, w)], np.uint32)
+        q2 = DeviceBuffer.zeroed(s, x.size, np.int8)
+        sc2 = DeviceBuffer.zeroed(s, x.size // w, np.float32)
+        mod.quantize_with_max(s, cfg(x.size), dev(s, x), w, dev(s, mx), q2, sc2)
+        assert np.array_equal(q2.to_host_vec(s), fixtures.tensor(c, "q").reshape(-1))
+        assert np.array_equal(bits(sc2.to_host_vec(s)), bits(fixtures.tensor(c, "scale").reshape(-1)))
+
+
+@pytest.mark.parametrize("width", [16, 128, 1000, 1001, 4096, 12288, 16400, 20000])
+def test_quantize_widths_edges_and_bf16(env, width):
+    ctx, mod, s = env
+    rng = np.random.default_rng(width)
+    m = 6
+    x = synth.student_t_rows(width, m, width)
+    x[1] = 0.0                                   # floor scale
+    x[2, :: max(1, width // 7)] = np.nan         # NaN ignored by the max, quantizes to 0
+    x[3, 5 % width] = np.inf                     # inf scale -> all zero codes
+    x[4] *= np.float32(1e-30)                    # tiny values
+    x[5, :4] = [127, -127, 0.5, -0.5][: min(4, width)]
+    for dtype in ("f32", "bf16"):
+        if dtype == "f32":
+            xin = x.reshape(-1)
+            wq, ws = oracle.quantize(xin, width)
+        else:
+            xin = (bits(x) >> 16).astype(np.uint16).reshape(-1)
+            wq, ws = oracle.quantize_bf16(xin, width)
+        q = DeviceBuffer.zeroed(s, m * width, np.int8)
+        sc = DeviceBuffer.zeroed(s, m, np.float32)
+        mod.quantize(s, rows(m, 1024), dev(s, xin), width, q, sc)
+        assert np.array_equal(q.to_host_vec(s), wq), dtype
+        assert np.array_equal(bits(sc.to_host_vec(s)), bits(ws)), dtype
+    del rng
+
+
+# ------------------------------------------------------------------ linear
+LINEAR_OPS = ("linear", "linear_dot4", "linear_mfma", "linear_prefill", "linear_splitk",
+              "linear_tiled", "linear_large")
+
+
+def test_linear_fixtures_every_kernel_family(env, fixtures):
+    ctx, mod, s = env
+    for c in fixtures.cases("linear"):
+        k = c["width"]
+        q, asc, w, ws = (dev(s, fixtures.tensor(c, key)) for key in ("q", "asc", "w", "ws"))
+        want = fixtures.tensor(c, "out").reshape(-1)
+        want_acc = fixtures.tensor(c, "acc").reshape(-1)
+        for op in LINEAR_OPS:
+            for dtype, expect in ((np.float32, bits(want)), (np.uint16, (bits(want) >> 16).astype(np.uint16)),
+                                  (np.int32, want_acc)):
+                out = DeviceBuffer.zeroed(s, want.size, dtype)
+                getattr(mod, op)(s, cfg(want.size * 32), q, asc, w, ws, k, out)
+                got = out.to_host_vec(s)
+                if dtype is np.float32:
+                    got = bits(got)
+                assert np.array_equal(got, expect), f"{op} {np.dtype(dtype)} {c['name']}"
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200, 256])
+def test_linear_random_shapes(env, m):
+    ctx, mod, s = env
+    rng = np.random.default_rng(1000 + m)
+    for n, k in ((1, 16), (17, 112), (33, 128), (100, 1040), (257, 4096), (64, 12288)):
+        if m * k * n > 64 * 12288 * 257:
+            continue
+        q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+        w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        if m > 1:
+            q[0] = 127
+            w[0] = -127
+        asc = (rng.random(m) / 64).astype(F32)
+        ws = (rng.random(n) / 64).astype(F32)
+        acc, out, outb = oracle.linear(q, asc, w, ws, k)
+        dq, da, dw, dws = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws)
+        for op in ("linear", "linear_dot4", "linear_mfma"):
+            o32 = DeviceBuffer.zeroed(s, m * n, np.int32)
+            getattr(mod, op)(s, None, dq, da, dw, dws, k, o32)
+            assert np.array_equal(o32.to_host_vec(s), acc), f"{op} acc m={m} n={n} k={k}"
+            ob = DeviceBuffer.zeroed(s, m * n, np.uint16)
+            getattr(mod, op)(s, None, dq, da, dw, dws, k, ob)
+            assert np.array_equal(ob.to_host_vec(s), outb), f"{op} bf16 m={m} n={n} k={k}"
+
+
+def test_linear_residual(env, fixtures):
+    ctx, mod, s = env
+    for c in fixtures.cases("linear"):
+        k = c["width"]
+        q, asc, w, ws = (dev(s, fixtures.tensor(c, key)) for key in ("q", "asc", "w", "ws"))
+        want = fixtures.tensor(c, "out").reshape(-1)
+        res = ((np.arange(want.size) % 17).astype(F32) - 8) * F32(0.0625)   # src/conformance.rs:236-241
+        comb_want = oracle.residual(res, want)
+        for dtype in (np.float32, np.uint16):
+            out = DeviceBuffer.zeroed(s, want.size, dtype)
+            comb = DeviceBuffer.zeroed(s, want.size, dtype)
+            mod.linear_residual(s, None, q, asc, w, ws, k, dev(s, res), out, comb, k)
+            o, cb = out.to_host_vec(s), comb.to_host_vec(s)
+            if dtype is np.float32:
+                assert np.array_equal(bits(o), bits(want)) and np.array_equal(bits(cb), bits(comb_want))
+            else:
+                assert np.array_equal(o, (bits(want) >> 16).astype(np.uint16))
+                assert np.array_equal(cb, (bits(comb_want) >> 16).astype(np.uint16))
+
+
+def test_pair_triple_share_activations(env, fixtures):
+    """src/conformance.rs:263-300: the same matrix in every sibling slot
+    reproduces the single projection bit for bit."""
+    ctx, mod, s = env
+    for c in fixtures.cases("linear"):
+        k = c["width"]
+        q, asc, w, ws = (dev(s, fixtures.tensor(c, key)) for key in ("q", "asc", "w", "ws"))
+        want = bits(fixtures.tensor(c, "out").reshape(-1))
+        outs = [DeviceBuffer.zeroed(s, want.size, np.float32) for _ in range(3)]
+        mod.linear_pair(s, None, q, asc, k, w, ws, outs[0], w, ws, outs[1])
+        assert all(np.array_equal(bits(o.to_host_vec(s)), want) for o in outs[:2])
+        outs = [DeviceBuffer.zeroed(s, want.size, np.float32) for _ in range(3)]
+        mod.linear_triple(s, None, q, asc, k, w, ws, outs[0], w, ws, outs[1], w, ws, outs[2])
+        assert all(np.array_equal(bits(o.to_host_vec(s)), want) for o in outs)
+
+
+@pytest.mark.parametrize("k,n", [(128, 33), (4096, 12288)])
+def test_gate_up_deterministic_inputs(env, k, n):
+    """Inputs of src/conformance.rs:746-777; gate/up bits equal separate
+    projections and the oracle."""
+    ctx, mod, s = env
+    i = np.arange(k, dtype=np.int64)
+    q = ((i * 13 % 255) - 127).astype(np.int8)
+    j = np.arange(k * n, dtype=np.int64)
+    w0 = ((j * 31 % 255) - 127).astype(np.int8)
+    w1 = ((j * 17 % 251) - 125).astype(np.int8)
+    asc = np.array([0.002], F32)
+    c = np.arange(n)
+    s0 = (F32(0.0001) * ((c % 7) + 1).astype(F32)).astype(F32)
+    s1 = (F32(0.0001) * ((c % 11) + 1).astype(F32)).astype(F32)
+    dq, da = dev(s, q), dev(s, asc)
+    dw0, dw1, ds0, ds1 = dev(s, w0), dev(s, w1), dev(s, s0), dev(s, s1)
+    g, u = DeviceBuffer.zeroed(s, n, np.float32), DeviceBuffer.zeroed(s, n, np.float32)
+    mod.linear_gate_up(s, rows((n + 7) // 8, 256), dq, da, k, dw0, ds0, g, dw1, ds1, u)
+    g1, u1 = DeviceBuffer.zeroed(s, n, np.float32), DeviceBuffer.zeroed(s, n, np.float32)
+    mod.linear(s, None, dq, da, dw0, ds0, k, g1)
+    mod.linear(s, None, dq, da, dw1, ds1, k, u1)
+    _, og, _ = oracle.linear(q, asc, w0, s0, k)
+    _, ou, _ = oracle.linear(q, asc, w1, s1, k)
+    assert np.array_equal(bits(g.to_host_vec(s)), bits(g1.to_host_vec(s)))
+    assert np.array_equal(bits(u.to_host_vec(s)), bits(u1.to_host_vec(s)))
+    assert np.array_equal(bits(g.to_host_vec(s)), bits(og))
+    assert np.array_equal(bits(u.to_host_vec(s)), bits(ou))
+
+
+# ------------------------------------------------------------------ selection
+def test_select_token_reference_cases(env):
+    ctx, mod, s = env
+    for x in argmax_cases() + [np.array([1, 3, 3], F32), np.array([np.nan], F32),
+                                np.array([np.inf], F32), np.array([-0.0, 0.0], F32)]:
+        out = DeviceBuffer.zeroed(s, 1, np.uint32)
+        mod.select_token(s, rows(1, 1024), dev(s, x), out)
+        assert int(out.to_host_vec(s)[0]) == argmax_expected(x), x[:8]
+    # empty input -> sentinel
+    out = DeviceBuffer.zeroed(s, 1, np.uint32)
+    empty = DeviceBuffer.zeroed(s, 0, np.float32)
+    mod.select_token(s, None, empty, out)
+    assert int(out.to_host_vec(s)[0]) == 0xFFFFFFFF
+
+
+def test_select_token_random_ties(env):
+    ctx, mod, s = env
+    rng = np.random.default_rng(77)
+    for n in (1, 63, 64, 65, 4095, 4097, 151936, 300001):
+        x = synth.bf16_round((rng.integers(-50, 50, n)).astype(F32) * F32(0.25))
+        out = DeviceBuffer.zeroed(s, 1, np.uint32)
+        mod.select_token(s, None, dev(s, x), out)
+        assert int(out.to_host_vec(s)[0]) == oracle.argmax(x) == int(np.argmax(x))
+
+
+@pytest.mark.parametrize("k", [4096, 12288, 1024])
+def test_linear_argmax_fused(env, k):
+    ctx, mod, s = env
+    rng = np.random.default_rng(k)
+    n = 20000 if k != 4096 else 151936
+    q = rng.integers(-127, 128, size=k, dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    w[n - 3] = 127 * np.sign(q).astype(np.int8)          # strong max ...
+    w[n // 3] = w[n - 3]                                  # ... tied at a lower index
+    ws = np.full(n, 0.004, F32)
+    asc = np.array([0.01], F32)
+    tok, logits = oracle.linear_argmax(q, asc, w, ws, k)
+    assert tok == n // 3
+    dq, da, dw, dws = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws)
+    for with_logits in (False, True):
+        t = DeviceBuffer.zeroed(s, 1, np.uint32)
+        lg = DeviceBuffer.zeroed(s, n, np.float32) if with_logits else None
+        mod.linear_argmax(s, dq, da, dw, dws, k, t, lg)
+        assert int(t.to_host_vec(s)[0]) == tok
+        if with_logits:
+            assert np.array_equal(bits(lg.to_host_vec(s)), bits(logits))
+    # a non-finite logit (scale overflow) gives the sentinel
+    ws2 = ws.copy()
+    ws2[5] = F32(3e38)
+    t = DeviceBuffer.zeroed(s, 1, np.uint32)
+    mod.linear_argmax(s, dq, da, dw, dev(s, ws2), k, t)
+    tok2, lg2 = oracle.linear_argmax(q, asc, w, ws2, k)
+    assert int(t.to_host_vec(s)[0]) == tok2
+    assert (tok2 == 0xFFFFFFFF) == (not np.all(np.isfinite(lg2)))
+
+
+# ------------------------------------------------------------------ graphs
+def test_graph_replay_matches_eager(env):
+    """Quantize -> linear -> fused lm_head argmax captured once and replayed
+    several times with eager work in between; every replay equals eager."""
+    ctx, mod, s = env
+    k, n, vocab = 4096, 4096, 32000
+    x = synth.normal_rows(5, 1, k).reshape(-1)
+    w = DeviceBuffer.zeroed(s, n * k, np.int8)
+    wh = DeviceBuffer.zeroed(s, vocab * k, np.int8)
+    ws = DeviceBuffer.zeroed(s, n, np.float32)
+    wsh = DeviceBuffer.zeroed(s, vocab, np.float32)
+    mod.synth_i8(s, w, 1, 11)
+    mod.synth_i8(s, wh, 1, 12)
+    mod.synth_f32(s, ws, 2, 11, 1e-3, 1e-2)
+    mod.synth_f32(s, wsh, 2, 12, 1e-3, 1e-2)
+    dx = dev(s, x)
+    q = DeviceBuffer.zeroed(s, k, np.int8)
+    sc = DeviceBuffer.zeroed(s, 1, np.float32)
+    h = DeviceBuffer.zeroed(s, n, np.float32)
+    q2 = DeviceBuffer.zeroed(s, n, np.int8)
+    sc2 = DeviceBuffer.zeroed(s, 1, np.float32)
+    tok = DeviceBuffer.zeroed(s, 1, np.uint32)
+    lg = DeviceBuffer.zeroed(s, vocab, np.uint16)
+
+    def step():
+        mod.quantize(s, None, dx, k, q, sc)
+        mod.linear(s, None, q, sc, w, ws, k, h)
+        mod.quantize(s, None, h, n, q2, sc2)
+        mod.linear_argmax(s, q2, sc2, wh, wsh, n, tok, lg)
+
+    step()
+    s.synchronize()
+    eager = (h.to_host_vec(s).copy(), lg.to_host_vec(s).copy(), int(tok.to_host_vec(s)[0]))
+    g = Graph(s)
+    with g:
+        step()
+    for rep in range(4):
+        for b in (h, lg, tok):
+            b.fill_zero(s)
+        g.launch()
+        s.synchronize()
+        assert np.array_equal(bits(h.to_host_vec(s)), bits(eager[0])), rep
+        assert np.array_equal(lg.to_host_vec(s), eager[1]), rep
+        assert int(tok.to_host_vec(s)[0]) == eager[2], rep
+        step()  # eager work between replays
+        s.synchronize()
+        assert int(tok.to_host_vec(s)[0]) == eager[2]
+
+
+# ------------------------------------------------------------------ synthetic
+def test_device_synth_matches_host_definition(env):
+    ctx, mod, s = env
+    n = (1 << 20) + 13
+    a = DeviceBuffer.zeroed(s, n, np.int8)
+    mod.synth_i8(s, a, 1, 1003)
+    got = a.to_host_vec(s)
+    assert np.array_equal(got, oracle.synth_i8(1, 1003, 0, n))
+    f = DeviceBuffer.zeroed(s, 4097, np.float32)
+    mod.synth_f32(s, f, 2, 1103, 1e-3, 1e-2)
+    assert np.array_equal(bits(f.to_host_vec(s)), bits(oracle.synth_f32(2, 1103, 0, 4097, 1e-3, 1e-2)))
+
+
+def test_errors_raise_not_fall_back(env):
+    ctx, mod, s = env
+    q = DeviceBuffer.zeroed(s, 4095, np.int8)
+    asc = DeviceBuffer.zeroed(s, 1, np.float32)
+    with pytest.raises(W8A8Error):
+        mod.linear(s, None, q, asc, q, asc, 4095, DeviceBuffer.zeroed(s, 1, np.float32))
