@@ -1,0 +1,338 @@
+"""Benchmark of the W8A8 linear-layer path on one MI355X.
+
+Headline (``value``): decode GEMV HBM throughput at M=1 over one token's
+worth of projections -- BASELINE configs 2 + 3: 36 layers x {qkv 6144x4096,
+o 4096x4096, gate_up 24576x4096, down 4096x12288} plus the W8A8 lm_head
+151936x4096 with fused greedy argmax -- all with distinct seeded weights
+(7.58 GB, far above the 256 MB MALL), activations already quantized to int8
+(the metric's byte formula counts int8 activations as the GEMV input).
+One step = those 145 launches, captured once in a hip graph and replayed.
+
+    bytes per projection = N*K + 4N + K + 4 + 2N   (weights, scales, q, s, bf16 out)
+    lm_head              = N*K + 4N + K + 4 + 4    (token instead of logits)
+
+Also reported (same JSON line): per-shape GEMV GB/s; the same step with a
+per-token quantize kernel before every projection; prefill INT8 TOPS at
+M=512 and HBM GB/s at M=129 on the four layer shapes (config 4); ragged
+M in {4,16,64} for the dot4 GEMV and the MFMA GEMM (config 5); the roofline
+of the dominant kernel; and the CPU baseline (the C oracle: quantize +
+integer GEMM + epilogue, OpenMP over output channels) timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+INT8_PEAK_TOPS = 5000.0        # MI355X dense INT8 MFMA, 5.0 POP/s
+SEED_W, SEED_S = 1, 2
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gemv_bytes(n: int, k: int, m: int = 1, out_bytes: int = 2) -> int:
+    return n * k + 4 * n + m * k + 4 * m + out_bytes * m * n
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extras", action="store_true", help="headline + roofline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode in this "
+              "build (the sharding design is described in DESIGN.md); run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    from inferrous_amd import CudaContext, DeviceBuffer, Event, Graph, load, synth
+
+    ctx = CudaContext(0)
+    cu, arch = ctx.info()
+    mod = load(ctx)
+    s = ctx.new_stream()
+    log(f"device {arch} with {cu} CUs")
+
+    # ------------------------------------------------------------ weights
+    t0 = time.time()
+    layers = []
+    for layer in range(synth.LAYERS):
+        mats = []
+        for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
+            w = DeviceBuffer.zeroed(s, n * k, np.int8)
+            ws = DeviceBuffer.zeroed(s, n, np.float32)
+            mod.synth_i8(s, w, SEED_W, synth.weight_stream(layer, si))
+            mod.synth_f32(s, ws, SEED_S, synth.scale_stream(layer, si), 1e-3, 1e-2)
+            mats.append((name, n, k, w, ws))
+        layers.append(mats)
+    hn, hk = synth.VOCAB, synth.HIDDEN
+    head_w = DeviceBuffer.zeroed(s, hn * hk, np.int8)
+    head_s = DeviceBuffer.zeroed(s, hn, np.float32)
+    mod.synth_i8(s, head_w, SEED_W, 9001)
+    mod.synth_f32(s, head_s, SEED_S, 9101, 1e-3, 1e-2)
+    s.synchronize()
+    weight_bytes = sum(n * k for (_, n, k, _, _) in layers[0]) * synth.LAYERS + hn * hk
+    log(f"generated {weight_bytes / 1e9:.2f} GB of int8 weights in {time.time() - t0:.1f}s")
+
+    # ------------------------------------------------------------ activations
+    xs, qs = {}, {}
+    for k, seed in ((4096, 40), (12288, 41)):
+        x = synth.normal_rows(seed, 1, k).reshape(-1)
+        xs[k] = DeviceBuffer.from_host(s, x)
+        q = DeviceBuffer.zeroed(s, k, np.int8)
+        sc = DeviceBuffer.zeroed(s, 1, np.float32)
+        mod.quantize(s, None, xs[k], k, q, sc)
+        qs[k] = (q, sc)
+    outs = {name: DeviceBuffer.zeroed(s, n, np.uint16) for (name, n, _, _, _) in layers[0]}
+    token = DeviceBuffer.zeroed(s, 1, np.uint32)
+
+    def decode_step(with_quant: bool = False):
+        for mats in layers:
+            for (name, n, k, w, ws) in mats:
+                q, sc = qs[k]
+                if with_quant:
+                    mod.quantize(s, None, xs[k], k, q, sc)
+                mod.linear(s, None, q, sc, w, ws, k, outs[name])
+        q, sc = qs[hk]
+        if with_quant:
+            mod.quantize(s, None, xs[hk], hk, q, sc)
+        mod.linear_argmax(s, q, sc, head_w, head_s, hk, token)
+
+    step_bytes = sum(gemv_bytes(n, k) for (_, n, k, _, _) in layers[0]) * synth.LAYERS \
+        + gemv_bytes(hn, hk, out_bytes=0) + 4
+
+    def capture(fn) -> Graph:
+        g = Graph(s)
+        with g:
+            fn()
+        return g
+
+    def time_graph(g: Graph, reps: int, warm: int = 2) -> float:
+        """Median-free mean over reps of graph replays, HIP events on `s` (ms)."""
+        for _ in range(warm):
+            g.launch()
+        s.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        for _ in range(reps):
+            g.launch()
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / reps
+
+    decode_step()          # eager pass: allocates the selection workspace outside capture
+    s.synchronize()
+    g_step = capture(decode_step)
+    for _ in range(args.warmup):
+        g_step.launch()
+    s.synchronize()
+    e0, e1 = Event(), Event()
+    t_start = time.perf_counter()
+    e0.record(s)
+    for _ in range(args.steps):
+        g_step.launch()
+    e1.record(s)
+    s.synchronize()
+    t_end = time.perf_counter()
+    wall_ms = (t_end - t_start) * 1e3 / args.steps
+    ev_ms = e0.elapsed_ms(e1) / args.steps
+    value = step_bytes / (wall_ms * 1e-3) / 1e9
+    log(f"decode step: {wall_ms * 1e3:.1f} us wall, {ev_ms * 1e3:.1f} us events, "
+        f"{value:.0f} GB/s ({value / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)")
+
+    # ------------------------------------------------------------ roofline
+    # Dominant kernel: the K=4096 M=1 GEMV (gemv_m1<4,4>) that serves qkv, o
+    # and gate_up -- 108 of the 145 launches and ~80% of the step's bytes.
+    def k4096_chain():
+        for mats in layers:
+            for (name, n, k, w, ws) in mats:
+                if k == 4096:
+                    q, sc = qs[k]
+                    mod.linear(s, None, q, sc, w, ws, k, outs[name])
+
+    g_dom = capture(k4096_chain)
+    dom_launches = 3 * synth.LAYERS
+    dom_bytes = sum(gemv_bytes(n, k) for (_, n, k, _, _) in layers[0] if k == 4096) * synth.LAYERS
+    dom_ms = time_graph(g_dom, max(10, args.steps // 2))
+    dom_avg_us = dom_ms * 1e3 / dom_launches
+    dom_gbs = dom_bytes / (dom_ms * 1e-3) / 1e9
+    roofline = {"kernel": "gemv_m1<4,4,0> (M=1, K=4096: qkv/o/gate_up)", "bound": "hbm",
+                "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "avg_launch_us": round(dom_avg_us, 3),
+                "bytes_per_launch": dom_bytes // dom_launches}
+    log(f"dominant GEMV: {dom_avg_us:.2f} us/launch avg, {dom_gbs:.0f} GB/s")
+
+    result = {
+        "metric": "decode GEMV HBM GB/s (% peak) at M=1; prefill INT8 TOPS (% peak) at M=512",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall_ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded int8 weights U[-127,127], f32 scales U[1e-3,1e-2], BF16 N(0,1) activations",
+        "config": {"workload": "C2+C3 decode: 36 x (qkv 6144x4096, o 4096x4096, gate_up 24576x4096, "
+                               "down 4096x12288) + W8A8 lm_head 151936x4096 + fused argmax, M=1",
+                   "bytes_per_step": step_bytes, "launches_per_step": 4 * synth.LAYERS + 1,
+                   "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
+                   "event_ms_per_step": round(ev_ms, 4)},
+        "roofline": roofline,
+    }
+
+    if not args.no_extras:
+        extras = {}
+        # per-shape GEMV throughput (36 launches each, distinct weights)
+        per = {}
+        for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
+            def chain(si=si):
+                for mats in layers:
+                    (nm, nn, kk, w, ws) = mats[si]
+                    q, sc = qs[kk]
+                    mod.linear(s, None, q, sc, w, ws, kk, outs[nm])
+            ms = time_graph(capture(chain), 20)
+            us = ms * 1e3 / synth.LAYERS
+            per[name] = {"us": round(us, 2), "GB/s": round(gemv_bytes(n, k) / (us * 1e-6) / 1e9, 1)}
+        ms = time_graph(capture(lambda: mod.linear_argmax(s, qs[hk][0], qs[hk][1], head_w, head_s,
+                                                          hk, token)), 20)
+        per["lm_head_argmax"] = {"us": round(ms * 1e3, 2),
+                                 "GB/s": round(gemv_bytes(hn, hk, out_bytes=0) / (ms * 1e-3) / 1e9, 1)}
+        extras["per_shape_gemv"] = per
+        log(f"per shape: {per}")
+        # step including a per-token quantize kernel before every projection
+        ms = time_graph(capture(lambda: decode_step(with_quant=True)), 20)
+        extras["decode_step_with_quantize"] = {"ms": round(ms, 4),
+                                               "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1)}
+        # prefill (config 4): M = 512 TOPS and M = 129 HBM GB/s, 36 layers x 4 shapes
+        pre = {}
+        for m in (512, 129):
+            pq = {}
+            for k, seed in ((4096, 700), (12288, 703)):
+                x = synth.student_t_rows(seed, m, k).reshape(-1)
+                q = DeviceBuffer.zeroed(s, m * k, np.int8)
+                sc = DeviceBuffer.zeroed(s, m, np.float32)
+                mod.quantize(s, None, DeviceBuffer.from_host(s, x), k, q, sc)
+                pq[k] = (q, sc)
+            pouts = {name: DeviceBuffer.zeroed(s, m * n, np.uint16) for (name, n, _, _, _) in layers[0]}
+
+            def prefill_chain(pq=pq, pouts=pouts):
+                for mats in layers:
+                    for (name, n, k, w, ws) in mats:
+                        mod.linear(s, None, pq[k][0], pq[k][1], w, ws, k, pouts[name])
+
+            ms = time_graph(capture(prefill_chain), 5, warm=1)
+            ops = sum(2 * m * n * k for (_, n, k, _, _) in layers[0]) * synth.LAYERS
+            byts = sum(gemv_bytes(n, k, m) for (_, n, k, _, _) in layers[0]) * synth.LAYERS
+            shp = {}
+            for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
+                def one(si=si, pq=pq, pouts=pouts):
+                    for mats in layers:
+                        (nm, nn, kk, w, ws) = mats[si]
+                        mod.linear(s, None, pq[kk][0], pq[kk][1], w, ws, kk, pouts[nm])
+                sms = time_graph(capture(one), 5, warm=1) / synth.LAYERS
+                shp[name] = {"us": round(sms * 1e3, 2),
+                             "TOPS": round(2 * m * n * k / (sms * 1e-3) / 1e12, 1)}
+            pre[f"M{m}"] = {"ms_36_layers": round(ms, 4),
+                            "TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                            "pct_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS * 100, 2),
+                            "GB/s": round(byts / (ms * 1e-3) / 1e9, 1),
+                            "pct_hbm_peak": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS * 100, 2),
+                            "per_shape": shp}
+            log(f"prefill M={m}: {pre[f'M{m}']}")
+        extras["prefill"] = pre
+        # ragged small batches (config 5): dot4 GEMV vs MFMA GEMM
+        rag = {}
+        for m in (1, 2, 4, 8, 16, 32, 64):
+            entry = {}
+            for si in (2, 3):
+                name, n, k = synth.DECODE_SHAPES[si]
+                x = synth.ragged_rows(range(9000 + 100 * m, 9000 + 100 * m + m), k).reshape(-1)
+                q = DeviceBuffer.zeroed(s, m * k, np.int8)
+                sc = DeviceBuffer.zeroed(s, m, np.float32)
+                mod.quantize(s, None, DeviceBuffer.from_host(s, x), k, q, sc)
+                o = DeviceBuffer.zeroed(s, m * n, np.uint16)
+                for fam in ("linear_dot4", "linear_mfma"):
+                    def chain(si=si, q=q, sc=sc, o=o, fam=fam, k=k):
+                        for mats in layers:
+                            (_, _, _, w, ws) = mats[si]
+                            getattr(mod, fam)(s, None, q, sc, w, ws, k, o)
+                    us = time_graph(capture(chain), 10) * 1e3 / synth.LAYERS
+                    entry[f"{name}_{fam.split('_')[1]}_GB/s"] = round(
+                        gemv_bytes(n, k, m) / (us * 1e-6) / 1e9, 1)
+            rag[f"M{m}"] = entry
+        extras["ragged"] = rag
+        log(f"ragged: {rag}")
+        result["extras"] = extras
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline() -> dict:
+    """The C oracle (quantize + exact integer GEMV + epilogue, OpenMP over
+    output channels) timed on this host over a bounded sample of the decode
+    workload: layer 0's four projections (193 MB of int8 weights)."""
+    import oracle
+    from inferrous_amd import synth
+
+    t0 = time.time()
+    nthreads = max(1, min(os.cpu_count() or 1, 16))
+    mats = []
+    for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
+        w = oracle.synth_i8(SEED_W, synth.weight_stream(0, si), 0, n * k)
+        ws = oracle.synth_f32(SEED_S, synth.scale_stream(0, si), 0, n, 1e-3, 1e-2)
+        mats.append((n, k, w, ws))
+    xs = {4096: synth.normal_rows(40, 1, 4096).reshape(-1), 12288: synth.normal_rows(41, 1, 12288).reshape(-1)}
+    sample_bytes = sum(gemv_bytes(n, k) for (n, k, _, _) in mats)
+    log(f"cpu baseline: host weights ready in {time.time() - t0:.1f}s")
+
+    def one_pass(threads: int) -> float:
+        t = time.perf_counter()
+        for (n, k, w, ws) in mats:
+            q, sc = oracle.quantize(xs[k], k)
+            oracle.linear(q, sc, w, ws, k, threads=threads)
+        return time.perf_counter() - t
+
+    res = {}
+    for threads in sorted({nthreads, 8, 1}, reverse=True):
+        one_pass(threads)
+        times = []
+        budget = time.perf_counter()
+        while len(times) < 5 or (time.perf_counter() - budget < 3.0 and len(times) < 50):
+            times.append(one_pass(threads))
+        med = float(np.median(times))
+        res[threads] = sample_bytes / med / 1e9
+        log(f"cpu baseline {threads} threads: {med * 1e3:.1f} ms/pass, {res[threads]:.2f} GB/s")
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(res[nthreads], 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "sample": (f"C oracle (quantize + int32 GEMV + BF16 epilogue) over layer 0's qkv/o/"
+                       f"gate_up/down at M=1 ({sample_bytes / 1e6:.1f} MB per pass), median of >=5 "
+                       f"passes; {cpu_model}; GB/s at 8 threads {res.get(8, 0):.3f}, at 1 thread "
+                       f"{res.get(1, 0):.3f}"),
+            "gbs_by_threads": {str(t): round(v, 3) for t, v in res.items()}}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

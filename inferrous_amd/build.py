@@ -49,7 +49,8 @@ def build(verbose: bool = False) -> Path:
         noise = "is not a recognized feature for this target"
         err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
         if r.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src}:\n{err}")
+            lines = [l for l in err.splitlines() if "error" in l][:20]
+            raise RuntimeError(f"hipcc failed for {src}:\n" + "\n".join(lines))
         if verbose and err.strip():
             print(err, file=sys.stderr)
         return obj

@@ -413,7 +413,10 @@ int w8a8_linear_grouped(void* stream, const int8_t* q, const float* asc, size_t 
   return W8A8_OK;
 }
 
-size_t w8a8_select_workspace_bytes(size_t n) { return 8 + 8 * (size_t)select_blocks(n); }
+size_t w8a8_select_workspace_bytes(size_t n) {
+  (void)n;
+  return kSelectSlots * sizeof(uint64_t);
+}
 
 int w8a8_select_token(void* stream, const float* x, size_t n, uint32_t* token, void* workspace,
                       size_t workspace_bytes) {
@@ -423,14 +426,12 @@ int w8a8_select_token(void* stream, const float* x, size_t n, uint32_t* token, v
   if (!workspace || workspace_bytes < w8a8_select_workspace_bytes(n)) return W8A8_EWORKSPACE;
   if (!al(x, 4) || !al(token, 4) || !al(workspace, 8)) return W8A8_EALIGN;
   if (!ready()) return W8A8_EINIT;
-  uint32_t* counter = (uint32_t*)workspace;
-  uint64_t* partials = (uint64_t*)workspace + 1;
-  return hip_status(launch_select((hipStream_t)stream, x, n, partials, counter, token));
+  return hip_status(launch_select((hipStream_t)stream, x, n, (uint64_t*)workspace, token));
 }
 
 size_t w8a8_linear_argmax_workspace_bytes(size_t n) {
-  // the k = 12288 configuration uses the most workgroups: an upper bound
-  return 8 + 8 * (size_t)gemv_argmax_blocks(n, 12288);
+  (void)n;
+  return kSelectSlots * sizeof(uint64_t);
 }
 
 int w8a8_linear_argmax(void* stream, const int8_t* q, const float* asc, const int8_t* w,
@@ -445,8 +446,7 @@ int w8a8_linear_argmax(void* stream, const int8_t* q, const float* asc, const in
     if (s != W8A8_OK) return s;
   }
   if (!al(token, 4)) return W8A8_EALIGN;
-  const size_t need = 8 + 8 * (size_t)gemv_argmax_blocks(n, k);
-  if (!workspace || workspace_bytes < need) return W8A8_EWORKSPACE;
+  if (!workspace || workspace_bytes < w8a8_linear_argmax_workspace_bytes(n)) return W8A8_EWORKSPACE;
   if (!al(workspace, 8)) return W8A8_EALIGN;
   if (!ready()) return W8A8_EINIT;
   GemvArgs a{};
@@ -460,8 +460,7 @@ int w8a8_linear_argmax(void* stream, const int8_t* q, const float* asc, const in
   a.n[0] = (uint32_t)n;
   a.out[0] = logits;
   a.out_dtype = logits ? logits_dtype : W8A8_OUT_F32;
-  a.counter = (uint32_t*)workspace;
-  a.partials = (uint64_t*)workspace + 1;
+  a.slots = (uint64_t*)workspace;
   a.token = token;
   return hip_status(launch_gemv_argmax((hipStream_t)stream, a));
 }

@@ -16,9 +16,10 @@
 // v_dot4_i32_i8, which keeps 16-24 KiB in flight per wave.  For M = 1 and
 // the Qwen3 widths (4096, 12288) the activation row lives in registers
 // (loaded once per wave from L2), so HBM traffic is the weights plus a few
-// bytes per row.  Partial sums are folded across lanes with a transposing
-// butterfly: R rows need log2(R) exchange steps that halve the values per
-// lane, then 6 - log2(R) plain steps -- instead of 6 R shuffles.
+// bytes per row.  Row-group indices are wave-uniform (scalar registers), so
+// sibling selection and row addressing cost scalar loads only.  Partial sums
+// are reduced with DPP row operations and v_readlane (no LDS round trips);
+// lanes 0..R-1 then write R consecutive outputs.
 //
 // INT32 sums are exact (|acc| <= 12288 * 127^2 < 2^31), so the lane/chunk
 // order is free; the epilogue keeps the reference's two RN multiplies and
@@ -33,26 +34,38 @@ constexpr int kGemvWaves = kGemvThreads / kWave;
 
 enum { EPI_PLAIN = 0, EPI_RESIDUAL = 1, EPI_ARGMAX = 2 };
 
-// Reduce V values per lane (V a power of two <= 64) across the wave.  On
-// return v[0] holds the full sum for value index lane / (64 / V) in every
-// lane whose low log2(64/V) bits are zero.
+// Sum of one int over the wave, returned wave-uniform (in an SGPR).  Within
+// each 16-lane row: quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror (DPP, no LDS traffic) leave the row sum in every
+// lane of the row; four v_readlane and scalar adds combine the rows.  i32
+// adds wrap, and every partial and final sum fits in i32, so it is exact.
+__device__ __forceinline__ int wave_sum_uniform(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, true);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+         __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+
+// Reduce V per-lane partial sums; lane i < V receives total i.
 template <int V>
-__device__ __forceinline__ int fold_reduce(int (&v)[V], int lane) {
-  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+__device__ __forceinline__ int reduce_to_lanes(const int (&v)[V], int lane) {
+  static_assert(V >= 1 && V <= 64, "at most one value per lane");
+  int out = 0;
 #pragma unroll
-  for (int width = V, off = 32; width > 1; width >>= 1, off >>= 1) {
-    const int half = width >> 1;
-    const bool upper = (lane & off) != 0;
-#pragma unroll
-    for (int j = 0; j < half; ++j) {
-      const int send = upper ? v[j] : v[j + half];
-      const int keep = upper ? v[j + half] : v[j];
-      v[j] = keep + __shfl_xor(send, off, kWave);
-    }
+  for (int i = 0; i < V; ++i) {
+    const int t = wave_sum_uniform(v[i]);
+    out = lane == i ? t : out;
   }
-#pragma unroll
-  for (int off = 32 / V; off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, kWave);
-  return v[0];
+  return out;
+}
+
+// Wave index inside the workgroup as a wave-uniform (scalar) value, so that
+// everything derived from it -- the owning sibling matrix, row addresses --
+// is computed and loaded through the scalar unit.
+__device__ __forceinline__ uint32_t wave_id() {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
 __device__ __forceinline__ void store_out(void* out, size_t idx, int dtype, int32_t acc, float value) {
@@ -73,12 +86,15 @@ __device__ __forceinline__ int owner(const GemvArgs& a, uint32_t g) {
   return mi;
 }
 
-// Last-workgroup reduction of per-workgroup selection keys.  `key` is this
-// thread's best key (0 = none).  Every thread of every workgroup must call it.
-__device__ __forceinline__ void select_finish(uint64_t key, uint64_t* partials, uint32_t* counter,
-                                              uint32_t* token) {
+// Greedy selection across workgroups.  Each workgroup reduces its keys in
+// LDS and folds its best into one of kSelectSlots device words with a single
+// device-scope atomicMax (slot = workgroup id mod kSelectSlots): no fences,
+// no spinning.  A one-wave finalize kernel, stream-ordered after the
+// producer, exchanges the slots back to zero and writes the token -- so the
+// workspace is left zeroed for the next call (graph-replay safe without a
+// memset).  Every thread of every workgroup must call select_publish.
+__device__ __forceinline__ void select_publish(uint64_t key, uint64_t* slots) {
   __shared__ uint64_t wbest[kGemvWaves];
-  __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   key = wave_max_u64(key);
   if (lane == 0) wbest[wave] = key;
@@ -87,36 +103,21 @@ __device__ __forceinline__ void select_finish(uint64_t key, uint64_t* partials, 
     uint64_t b = wbest[0];
 #pragma unroll
     for (int i = 1; i < kGemvWaves; ++i) b = wbest[i] > b ? wbest[i] : b;
-    __hip_atomic_store(&partials[blockIdx.x], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
-    const uint32_t prev = atomicAdd(counter, 1u);
-    last = (prev == gridDim.x - 1);
+    if (b) atomicMax((unsigned long long*)&slots[blockIdx.x % kSelectSlots], (unsigned long long)b);
   }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  uint64_t b = 0;
-  for (uint32_t i = threadIdx.x; i < gridDim.x; i += kGemvThreads) {
-    const uint64_t p = __hip_atomic_load(&partials[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    b = p > b ? p : b;
-  }
-  b = wave_max_u64(b);
-  if (lane == 0) wbest[wave] = b;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t f = wbest[0];
-#pragma unroll
-    for (int i = 1; i < kGemvWaves; ++i) f = wbest[i] > f ? wbest[i] : f;
-    *token = key_to_token(f);
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+}
+
+__global__ __launch_bounds__(64) void select_finalize(uint64_t* slots, uint32_t* token) {
+  uint64_t v = atomicExch((unsigned long long*)&slots[threadIdx.x], 0ull);
+  v = wave_max_u64(v);
+  if (threadIdx.x == 0) *token = key_to_token(v);
 }
 
 // M = 1, k = KC * 1024 known at compile time: activations held in registers.
 template <int R, int KC, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void gemv_m1(GemvArgs a) {
   const int lane = threadIdx.x & 63;
-  const uint32_t g = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
+  const uint32_t g = blockIdx.x * kGemvWaves + wave_id();
   const bool live = g < a.gbegin[a.count];
   const int mi = live ? owner(a, g) : 0;
   const uint32_t n = a.n[mi];
@@ -144,10 +145,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_m1(GemvArgs a) {
 #pragma unroll
       for (int c = 0; c < KC; ++c) acc[r] = dot16(x[c], wv[r][c], acc[r]);
   }
-  const int total = fold_reduce<R>(acc, lane);
-  constexpr int kSpan = 64 / R;
-  const uint32_t row = row0 + lane / kSpan;
-  const bool writer = live && (lane % kSpan) == 0 && row < n;
+  const int total = reduce_to_lanes<R>(acc, lane);
+  const uint32_t row = row0 + lane;
+  const bool writer = live && lane < R && row < n;
   float value = 0.f;
   if (writer) {
     value = dequant(total, a.asc[0], a.ws[mi][row]);
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_m1(GemvArgs a) {
     }
   }
   if (EPI == EPI_ARGMAX)
-    select_finish(writer ? select_key(value, row) : 0ull, a.partials, a.counter, a.token);
+    select_publish(writer ? select_key(value, row) : 0ull, a.slots);
 }
 
 // Any m (blockIdx.y selects MT activation rows), any k % 16 == 0.
@@ -166,7 +166,7 @@ template <int R, int MT, int U, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
   constexpr int V = R * MT;
   const int lane = threadIdx.x & 63;
-  const uint32_t g = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
+  const uint32_t g = blockIdx.x * kGemvWaves + wave_id();
   const bool live = g < a.gbegin[a.count];
   const int mi = live ? owner(a, g) : 0;
   const uint32_t n = a.n[mi];
@@ -179,9 +179,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
   for (int i = 0; i < V; ++i) acc[i] = 0;
   if (live) {
     const int8_t* __restrict__ W = a.w[mi];
-    size_t wrow[R];
+    const int8_t* wrow[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) wrow[r] = (size_t)min(row0 + r, n - 1) * K;
+    for (int r = 0; r < R; ++r) wrow[r] = W + (size_t)min(row0 + r, n - 1) * K;
     const int8_t* xrow[MT];
     bool xok[MT];
 #pragma unroll
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
         const uint32_t kk = (c + u) * 1024 + lane * 16;
         const bool ok = (c + u < nch) && kk < K;
 #pragma unroll
-        for (int r = 0; r < R; ++r) wv[u][r] = ok ? load_nt16(W + wrow[r] + kk) : v4i{0, 0, 0, 0};
+        for (int r = 0; r < R; ++r) wv[u][r] = ok ? load_nt16(wrow[r] + kk) : v4i{0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < MT; ++t) xv[u][t] = (ok && xok[t]) ? load16(xrow[t] + kk) : v4i{0, 0, 0, 0};
       }
@@ -209,12 +209,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
           for (int r = 0; r < R; ++r) acc[t * R + r] = dot16(xv[u][t], wv[u][r], acc[t * R + r]);
     }
   }
-  const int total = fold_reduce<V>(acc, lane);
-  constexpr int kSpan = 64 / V;
-  const int idx = lane / kSpan;
-  const uint32_t t = m0 + idx / R;
-  const uint32_t row = row0 + idx % R;
-  const bool writer = live && (lane % kSpan) == 0 && row < n && t < a.m;
+  const int total = reduce_to_lanes<V>(acc, lane);
+  const uint32_t t = m0 + lane / R;
+  const uint32_t row = row0 + lane % R;
+  const bool writer = live && lane < V && row < n && t < a.m;
   float value = 0.f;
   if (writer) {
     value = dequant(total, a.asc[t], a.ws[mi][row]);
@@ -226,20 +224,19 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
     }
   }
   if (EPI == EPI_ARGMAX)
-    select_finish(writer ? select_key(value, row) : 0ull, a.partials, a.counter, a.token);
+    select_publish(writer ? select_key(value, row) : 0ull, a.slots);
 }
 
 // Standalone greedy selection over f32 values.
 __global__ __launch_bounds__(kGemvThreads) void select_kernel(const float* __restrict__ x, size_t n,
-                                                               uint64_t* partials, uint32_t* counter,
-                                                               uint32_t* token) {
+                                                               uint64_t* slots) {
   uint64_t best = 0;
   for (size_t i = (size_t)blockIdx.x * kGemvThreads + threadIdx.x; i < n;
        i += (size_t)gridDim.x * kGemvThreads) {
     const uint64_t k = select_key(x[i], (uint32_t)i);
     best = k > best ? k : best;
   }
-  select_finish(best, partials, counter, token);
+  select_publish(best, slots);
 }
 
 __global__ void write_sentinel(uint32_t* token) {
@@ -311,34 +308,28 @@ hipError_t launch_gemv(hipStream_t st, GemvArgs& a) {
   return dispatch<EPI_PLAIN>(st, a);
 }
 
-// Number of workgroups the fused lm_head launch uses for n rows at width k.
-uint32_t gemv_argmax_blocks(size_t n, uint32_t k) {
-  const uint32_t R = (k == 12288) ? 2 : 4;
-  const uint64_t groups = (n + R - 1) / R;
-  return (uint32_t)((groups + kGemvWaves - 1) / kGemvWaves);
-}
-
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
   if (a.n[0] == 0) {
     hipLaunchKernelGGL(write_sentinel, dim3(1), dim3(64), 0, st, a.token);
     return hipGetLastError();
   }
-  return dispatch<EPI_ARGMAX>(st, a);
+  hipError_t e = dispatch<EPI_ARGMAX>(st, a);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kSelectSlots), 0, st, a.slots, a.token);
+  return hipGetLastError();
 }
 
-uint32_t select_blocks(size_t n) {
-  const uint64_t b = (n + kGemvThreads * 16 - 1) / (kGemvThreads * 16);
-  return (uint32_t)(b < 1 ? 1 : (b > 1024 ? 1024 : b));
-}
-
-hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* partials,
-                         uint32_t* counter, uint32_t* token) {
+hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* slots, uint32_t* token) {
   if (n == 0) {
     hipLaunchKernelGGL(write_sentinel, dim3(1), dim3(64), 0, st, token);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(select_kernel, dim3(select_blocks(n)), dim3(kGemvThreads), 0, st, x, n,
-                     partials, counter, token);
+  const uint64_t b = (n + kGemvThreads * 16 - 1) / (kGemvThreads * 16);
+  const unsigned blocks = (unsigned)(b > 1024 ? 1024 : b);
+  hipLaunchKernelGGL(select_kernel, dim3(blocks), dim3(kGemvThreads), 0, st, x, n, slots);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kSelectSlots), 0, st, slots, token);
   return hipGetLastError();
 }
 

@@ -10,6 +10,7 @@
 namespace w8a8 {
 
 constexpr int kMaxGroup = 4;
+constexpr int kSelectSlots = 64;  // selection workspace: 64 x u64, zero when idle
 
 // One GEMV launch: up to kMaxGroup sibling projections sharing q/asc.
 struct GemvArgs {
@@ -25,8 +26,7 @@ struct GemvArgs {
   int out_dtype;
   const float* residual;  // EPI residual (count == 1)
   void* combined;
-  uint64_t* partials;  // fused selection (count == 1, m == 1)
-  uint32_t* counter;
+  uint64_t* slots;  // fused selection (count == 1, m == 1): kSelectSlots words
   uint32_t* token;
 };
 
@@ -51,10 +51,7 @@ hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);
-uint32_t gemv_argmax_blocks(size_t n, uint32_t k);
-hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* partials,
-                         uint32_t* counter, uint32_t* token);
-uint32_t select_blocks(size_t n);
+hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* slots, uint32_t* token);
 
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a);
 
