@@ -415,7 +415,7 @@ int w8a8_linear_grouped(void* stream, const int8_t* q, const float* asc, size_t 
 
 size_t w8a8_select_workspace_bytes(size_t n) {
   (void)n;
-  return kSelectSlots * sizeof(uint64_t);
+  return kSelectSlots * kSelectStride * sizeof(uint64_t);
 }
 
 int w8a8_select_token(void* stream, const float* x, size_t n, uint32_t* token, void* workspace,
@@ -431,7 +431,7 @@ int w8a8_select_token(void* stream, const float* x, size_t n, uint32_t* token, v
 
 size_t w8a8_linear_argmax_workspace_bytes(size_t n) {
   (void)n;
-  return kSelectSlots * sizeof(uint64_t);
+  return kSelectSlots * kSelectStride * sizeof(uint64_t);
 }
 
 int w8a8_linear_argmax(void* stream, const int8_t* q, const float* asc, const int8_t* w,

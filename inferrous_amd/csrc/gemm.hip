@@ -14,12 +14,22 @@
 // sum unchanged, so both operands are read with the same lane -> k map; the
 // 4 x i32 result of lane l holds rows 4*(l/16)+v, column l%16.
 //
-// Two kernels:
+// Three kernels:
+//  * gemm_dma (M > 64, k % 64 == 0): the prefill GEMM, built on
+//    v_mfma_i32_32x32x32_i8 (on gfx950 the 16x16x64 int8 form issues at half
+//    its rate).  Operands move global -> LDS with global_load_lds_dwordx4
+//    (no VGPR staging) through an S-stage ring, one barrier per 64-byte K
+//    stage.  Each wave-wide DMA moves 16 rows x 64 bytes with four adjacent
+//    lanes per row (coalesced); the 16-byte chunk order inside each row is
+//    XOR-swizzled with g(r) = ((r >> 1) ^ (r >> 2)) & 3 so the MFMA fragment
+//    reads (row = lane % 32, chunk = 2s + lane / 32) are bank-conflict free.
+//    Workgroups are numbered XCD-aware (below).  Tile shape per problem is
+//    chosen by the host (measured: large N -> 256 x 192, else 64 x 128).
 //  * gemm_skinny (M <= 64, HBM-bound): one workgroup owns 16 weight rows;
 //    its S waves split K and stream their weight fragments straight from
 //    HBM into MFMA B operands (no LDS round trip), activation fragments come
 //    from L1/L2.  Partial i32 tiles are summed through LDS -- exact.
-//  * gemm_tiled (M > 64): BM x BN output tile, 4 waves, 128-byte K stages
+//  * gemm_tiled (M > 64 with k % 64 != 0): BM x BN output tile, 4 waves, 128-byte K stages
 //    double-buffered in LDS (row pitch 144 B: a 16-lane ds_read_b128 column
 //    touches every bank once), global loads of stage k+1 in flight while
 //    stage k feeds the MFMAs.  Workgroups are numbered so that the M tiles
@@ -204,6 +214,162 @@ __global__ __launch_bounds__(256) void gemm_tiled(GemmArgs a, uint32_t tiles_m, 
       }
 }
 
+// ---------------------------------------------------------------- dma
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// s_waitcnt with vmcnt = N and the other counters left at their maximum
+// (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+#define W8A8_LDS_PTR(p) ((void __attribute__((address_space(3)))*)(p))
+
+// Epilogue modes, resolved at compile time so the unrolled store loop stays
+// branch-free: raw accumulators, f32 or BF16 outputs, each optionally with
+// the residual sum bf(residual + out).
+enum { EP_I32 = 0, EP_F32 = 1, EP_BF16 = 2, EP_F32_RES = 3, EP_BF16_RES = 4 };
+
+template <int EP>
+__device__ __forceinline__ void store_ep(const GemmArgs& a, uint32_t r, uint32_t c, int32_t acc, float wsc) {
+  const size_t o = (size_t)r * a.n + c;
+  if (EP == EP_I32) {
+    reinterpret_cast<int32_t*>(a.out)[o] = acc;
+    return;
+  }
+  const float v = dequant(acc, a.asc[r], wsc);
+  if (EP == EP_F32 || EP == EP_F32_RES) {
+    if (a.out) reinterpret_cast<float*>(a.out)[o] = v;
+    if (EP == EP_F32_RES) reinterpret_cast<float*>(a.combined)[o] = bf16_rne(a.residual[o] + v);
+  } else {
+    if (a.out) reinterpret_cast<uint16_t*>(a.out)[o] = (uint16_t)(__float_as_uint(v) >> 16);
+    if (EP == EP_BF16_RES)
+      reinterpret_cast<uint16_t*>(a.combined)[o] = (uint16_t)(__float_as_uint(bf16_rne(a.residual[o] + v)) >> 16);
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int S, int EP>
+__global__ __launch_bounds__(256) void gemm_dma(GemmArgs a, uint32_t tiles_m, uint32_t tiles_n) {
+  constexpr int WAVES_N = BN / WN;
+  static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
+  static_assert(WM % 32 == 0 && WN % 32 == 0 && S >= 2 && S <= 6, "tile shape");
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int AB = BM / 16, BB = BN / 16;  // 1 KiB DMA blocks (16 rows x 64 B) per stage
+  constexpr int NB = AB + BB;
+  static_assert(NB % 4 == 0, "DMA blocks divide among the four waves");
+  constexpr int L = NB / 4;                  // DMA loads per wave per stage
+  constexpr int STAGE = NB * 1024;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+
+  const uint32_t T = tiles_m * tiles_n;
+  uint32_t Lt = blockIdx.x;
+  if (T % 8 == 0) Lt = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8;
+  const uint32_t m0 = (Lt % tiles_m) * BM, n0 = (Lt / tiles_m) * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
+  const uint32_t K = a.k, KT = K / 64;
+
+  // Sources of this wave's DMA blocks; rows past M / N re-read row 0 (their
+  // products only reach accumulator cells that are never stored).
+  const int8_t* src[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    const int b = wave * L + j;
+    const int rr = lane >> 2, cc = (lane & 3) ^ lds_swizzle(rr);
+    const bool isA = b < AB;
+    const uint32_t row = (isA ? m0 + b * 16 : n0 + (b - AB) * 16) + rr;
+    const uint32_t lim = isA ? a.m : a.n;
+    src[j] = (isA ? a.q : a.w) + (size_t)(row < lim ? row : 0) * K + cc * 16;
+  }
+  auto issue = [&](uint32_t kt) {
+    int8_t* base = lds + (kt % S) * STAGE;
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(src[j] + (size_t)kt * 64),
+                                       W8A8_LDS_PTR(base + (wave * L + j) * 1024 + lane * 16), 16, 0, 0);
+  };
+  const int fr = lane & 31, fhalf = lane >> 5;
+  int foff[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    foff[s] = (fr >> 4) * 1024 + (4 * (fr & 15) + ((2 * s + fhalf) ^ lds_swizzle(fr & 15))) * 16;
+
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < (int)KT) issue(s);
+  for (uint32_t kt = 0; kt < KT; ++kt) {
+    // Stage kt must have landed: of this wave's outstanding DMA groups only
+    // the ones issued after it (stages kt+1 .. min(KT-1, kt+S-2)) may remain.
+    const uint32_t newer = min(KT - 1, kt + S - 2) - kt;
+    if (newer >= (uint32_t)(S - 2)) wait_vmcnt<(S - 2) * L>();
+    else if (newer == 3) wait_vmcnt<3 * L>();
+    else if (newer == 2) wait_vmcnt<2 * L>();
+    else if (newer == 1) wait_vmcnt<L>();
+    else wait_vmcnt<0>();
+    // all waves' parts of stage kt are in LDS, and every wave has finished
+    // reading stage kt-1, whose buffer the next DMA overwrites
+    __builtin_amdgcn_s_barrier();
+    if (kt + S - 1 < KT) issue(kt + S - 1);
+    const int8_t* base = lds + (kt % S) * STAGE;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      v4i af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = *(const v4i*)(base + ((wm0 / 32 + i) * 2) * 1024 + foff[s]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(base + (AB + (wn0 / 32 + j) * 2) * 1024 + foff[s]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
+    }
+  }
+  // 32x32 result layout: lane l, value v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const uint32_t c = n0 + wn0 + j * 32 + (lane & 31);
+    const float wsc = (EP != EP_I32 && c < a.n) ? a.ws[c] : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const uint32_t r = m0 + wm0 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (r < a.m && c < a.n) store_ep<EP>(a, r, c, acc[i][j][v], wsc);
+      }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+static void launch_dma(hipStream_t st, const GemmArgs& a) {
+  const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
+  const dim3 grid(tm * tn), block(256);
+  if (a.out_dtype == W8A8_OUT_I32)
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_I32>), grid, block, 0, st, a, tm, tn);
+  else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32_RES>), grid, block, 0, st, a, tm, tn);
+  else if (a.out_dtype == W8A8_OUT_F32)
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32>), grid, block, 0, st, a, tm, tn);
+  else if (a.residual)
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16_RES>), grid, block, 0, st, a, tm, tn);
+  else
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16>), grid, block, 0, st, a, tm, tn);
+}
+
 // ---------------------------------------------------------------- dispatch
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   if (a.m == 0 || a.n == 0) return hipSuccess;
@@ -214,6 +380,14 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
     hipLaunchKernelGGL((gemm_skinny<2, 4, 4>), dim3(nb16, 1), dim3(256), 0, st, a);
   } else if (a.m <= 64) {
     hipLaunchKernelGGL((gemm_skinny<4, 4, 2>), dim3(nb16, 1), dim3(256), 0, st, a);
+  } else if (a.k % 64 == 0) {
+    // measured on MI355X (Qwen3-8B shapes at M = 129 and 512)
+    if (a.n >= 16384 && a.m >= 256)
+      launch_dma<256, 192, 128, 96, 4>(st, a);
+    else if (a.n >= 16384)
+      launch_dma<128, 192, 64, 96, 5>(st, a);
+    else
+      launch_dma<64, 128, 32, 64, 6>(st, a);
   } else {
     constexpr int BM = 128, BN = 128;
     const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;

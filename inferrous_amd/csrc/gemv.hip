@@ -12,8 +12,9 @@
 // non-temporal loads: one wave (64 lanes) owns R consecutive output rows and
 // splits k into 1 KiB chunks, lane l reading bytes [l*16, l*16+16) of each
 // chunk, so every wave-wide load is one contiguous, fully coalesced 1 KiB
-// segment.  All R x chunks loads of a row group are issued before the first
-// v_dot4_i32_i8, which keeps 16-24 KiB in flight per wave.  For M = 1 and
+// segment.  A wave issues the loads of its whole row group (one or two rows,
+// 4-12 KiB) up front, reduces, writes and exits; the hardware dispatcher then
+// walks the matrix in address order.  For M = 1 and
 // the Qwen3 widths (4096, 12288) the activation row lives in registers
 // (loaded once per wave from L2), so HBM traffic is the weights plus a few
 // bytes per row.  Row-group indices are wave-uniform (scalar registers), so
@@ -86,14 +87,25 @@ __device__ __forceinline__ int owner(const GemvArgs& a, uint32_t g) {
   return mi;
 }
 
-// Greedy selection across workgroups.  Each workgroup reduces its keys in
-// LDS and folds its best into one of kSelectSlots device words with a single
-// device-scope atomicMax (slot = workgroup id mod kSelectSlots): no fences,
-// no spinning.  A one-wave finalize kernel, stream-ordered after the
-// producer, exchanges the slots back to zero and writes the token -- so the
-// workspace is left zeroed for the next call (graph-replay safe without a
-// memset).  Every thread of every workgroup must call select_publish.
-__device__ __forceinline__ void select_publish(uint64_t key, uint64_t* slots) {
+// Greedy selection across workgroups.  Every output row's key is folded
+// into one of kSelectSlots device words (slot = row mod kSelectSlots, one
+// 128-byte line apart) by the lane that computed it -- no barrier, no fence,
+// no spinning.  A slot only grows while the producer runs, so the lane first
+// reads it (device-coherent relaxed load) and issues the atomicMax only when
+// its key is larger: a stale read can cause a redundant atomic, never a
+// missed one, and on typical data almost every row skips the atomic.  A
+// one-wave finalize kernel, stream-ordered after the producer, exchanges the
+// slots back to zero and writes the token, leaving the workspace zeroed for
+// the next call (graph-replay safe without a memset).
+__device__ __forceinline__ void select_publish_lane(uint64_t key, uint32_t row, uint64_t* slots) {
+  uint64_t* sp = &slots[(row % kSelectSlots) * kSelectStride];
+  if (key > __hip_atomic_load(sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    atomicMax((unsigned long long*)sp, (unsigned long long)key);
+}
+
+// Workgroup-level variant for the standalone selection kernel (few, large
+// workgroups): reduce in LDS first, then one atomic per workgroup.
+__device__ __forceinline__ void select_publish_block(uint64_t key, uint64_t* slots) {
   __shared__ uint64_t wbest[kGemvWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   key = wave_max_u64(key);
@@ -103,12 +115,12 @@ __device__ __forceinline__ void select_publish(uint64_t key, uint64_t* slots) {
     uint64_t b = wbest[0];
 #pragma unroll
     for (int i = 1; i < kGemvWaves; ++i) b = wbest[i] > b ? wbest[i] : b;
-    if (b) atomicMax((unsigned long long*)&slots[blockIdx.x % kSelectSlots], (unsigned long long)b);
+    select_publish_lane(b, blockIdx.x, slots);
   }
 }
 
 __global__ __launch_bounds__(64) void select_finalize(uint64_t* slots, uint32_t* token) {
-  uint64_t v = atomicExch((unsigned long long*)&slots[threadIdx.x], 0ull);
+  uint64_t v = atomicExch((unsigned long long*)&slots[threadIdx.x * kSelectStride], 0ull);
   v = wave_max_u64(v);
   if (threadIdx.x == 0) *token = key_to_token(v);
 }
@@ -157,8 +169,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_m1(GemvArgs a) {
       store_out(a.combined, row, a.out_dtype, total, comb);
     }
   }
-  if (EPI == EPI_ARGMAX)
-    select_publish(writer ? select_key(value, row) : 0ull, a.slots);
+  if (EPI == EPI_ARGMAX && writer) select_publish_lane(select_key(value, row), row, a.slots);
 }
 
 // Any m (blockIdx.y selects MT activation rows), any k % 16 == 0.
@@ -223,8 +234,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
       store_out(a.combined, o, a.out_dtype, total, comb);
     }
   }
-  if (EPI == EPI_ARGMAX)
-    select_publish(writer ? select_key(value, row) : 0ull, a.slots);
+  if (EPI == EPI_ARGMAX && writer) select_publish_lane(select_key(value, row), row, a.slots);
 }
 
 // Standalone greedy selection over f32 values.
@@ -236,7 +246,7 @@ __global__ __launch_bounds__(kGemvThreads) void select_kernel(const float* __res
     const uint64_t k = select_key(x[i], (uint32_t)i);
     best = k > best ? k : best;
   }
-  select_publish(best, slots);
+  select_publish_block(best, slots);
 }
 
 __global__ void write_sentinel(uint32_t* token) {
@@ -255,52 +265,43 @@ static uint32_t count_groups(GemvArgs& a, const uint32_t* n, int count) {
   return g;
 }
 
+template <int R, int KC, int EPI>
+static hipError_t launch_m1(hipStream_t st, GemvArgs& a, const uint32_t* nn) {
+  const uint32_t groups = count_groups<R>(a, nn, a.count);
+  if (groups == 0) return hipSuccess;
+  hipLaunchKernelGGL((gemv_m1<R, KC, EPI>), dim3((groups + kGemvWaves - 1) / kGemvWaves),
+                     dim3(kGemvThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int MT, int U, int EPI>
+static hipError_t launch_mt(hipStream_t st, GemvArgs& a, const uint32_t* nn) {
+  const uint32_t groups = count_groups<4>(a, nn, a.count);
+  if (groups == 0) return hipSuccess;
+  hipLaunchKernelGGL((gemv_mt<4, MT, U, EPI>),
+                     dim3((groups + kGemvWaves - 1) / kGemvWaves, (a.m + MT - 1) / MT),
+                     dim3(kGemvThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+// Row-group shape: measured on MI355X, waves that issue one short batch
+// (one or two 4 KiB rows) and exit stream HBM better than longer batches or
+// grid-stride sweeps; two rows per wave helps only the small matrices.
 template <int EPI>
 static hipError_t dispatch(hipStream_t st, GemvArgs& a) {
   uint32_t nn[kMaxGroup];
-  for (int i = 0; i < a.count; ++i) nn[i] = a.n[i];
-  // M = 1 at the Qwen3 widths: activation row register-resident.
-  if (a.m == 1 && a.k == 4096) {
-    const uint32_t groups = count_groups<4>(a, nn, a.count);
-    if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemv_m1<4, 4, EPI>), dim3((groups + kGemvWaves - 1) / kGemvWaves),
-                       dim3(kGemvThreads), 0, st, a);
-    return hipGetLastError();
+  uint64_t total = 0;
+  for (int i = 0; i < a.count; ++i) {
+    nn[i] = a.n[i];
+    total += a.n[i];
   }
-  if (a.m == 1 && a.k == 12288) {
-    const uint32_t groups = count_groups<2>(a, nn, a.count);
-    if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemv_m1<2, 12, EPI>), dim3((groups + kGemvWaves - 1) / kGemvWaves),
-                       dim3(kGemvThreads), 0, st, a);
-    return hipGetLastError();
-  }
-  if (a.m == 1 || EPI == EPI_ARGMAX) {
-    const uint32_t groups = count_groups<4>(a, nn, a.count);
-    if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemv_mt<4, 1, 4, EPI>), dim3((groups + kGemvWaves - 1) / kGemvWaves),
-                       dim3(kGemvThreads), 0, st, a);
-    return hipGetLastError();
-  }
-  if (a.m <= 2) {
-    const uint32_t groups = count_groups<4>(a, nn, a.count);
-    if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemv_mt<4, 2, 4, EPI>), dim3((groups + kGemvWaves - 1) / kGemvWaves, 1),
-                       dim3(kGemvThreads), 0, st, a);
-    return hipGetLastError();
-  }
-  if (a.m <= 4) {
-    const uint32_t groups = count_groups<4>(a, nn, a.count);
-    if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL((gemv_mt<4, 4, 2, EPI>), dim3((groups + kGemvWaves - 1) / kGemvWaves, 1),
-                       dim3(kGemvThreads), 0, st, a);
-    return hipGetLastError();
-  }
-  const uint32_t groups = count_groups<4>(a, nn, a.count);
-  if (groups == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_mt<4, 8, 2, EPI>),
-                     dim3((groups + kGemvWaves - 1) / kGemvWaves, (a.m + 7) / 8), dim3(kGemvThreads),
-                     0, st, a);
-  return hipGetLastError();
+  if (a.m == 1 && a.k == 4096)
+    return total <= 8192 ? launch_m1<2, 4, EPI>(st, a, nn) : launch_m1<1, 4, EPI>(st, a, nn);
+  if (a.m == 1 && a.k == 12288) return launch_m1<1, 12, EPI>(st, a, nn);
+  if (a.m == 1 || EPI == EPI_ARGMAX) return launch_mt<1, 4, EPI>(st, a, nn);
+  if (a.m <= 2) return launch_mt<2, 4, EPI>(st, a, nn);
+  if (a.m <= 4) return launch_mt<4, 2, EPI>(st, a, nn);
+  return launch_mt<8, 2, EPI>(st, a, nn);
 }
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a) {

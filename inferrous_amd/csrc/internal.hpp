@@ -10,7 +10,8 @@
 namespace w8a8 {
 
 constexpr int kMaxGroup = 4;
-constexpr int kSelectSlots = 64;  // selection workspace: 64 x u64, zero when idle
+constexpr int kSelectSlots = 64;   // selection workspace: 64 u64 slots, zero when idle,
+constexpr int kSelectStride = 16;  // one 128-byte line apart (stride in u64 units)
 
 // One GEMV launch: up to kMaxGroup sibling projections sharing q/asc.
 struct GemvArgs {
@@ -26,7 +27,7 @@ struct GemvArgs {
   int out_dtype;
   const float* residual;  // EPI residual (count == 1)
   void* combined;
-  uint64_t* slots;  // fused selection (count == 1, m == 1): kSelectSlots words
+  uint64_t* slots;  // fused selection (count == 1, m == 1)
   uint32_t* token;
 };
 

@@ -266,6 +266,24 @@ def test_linear_argmax_fused(env, k):
     assert (tok2 == 0xFFFFFFFF) == (not np.all(np.isfinite(lg2)))
 
 
+def test_linear_argmax_consecutive_calls_smaller_max(env):
+    """The selection slots are reused across calls: a call whose maximum is
+    far below the previous call's must still find its own token."""
+    ctx, mod, s = env
+    rng = np.random.default_rng(99)
+    k, n = 4096, 50000
+    q = rng.integers(-127, 128, size=k, dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    dq, dw = dev(s, q), dev(s, w)
+    tok = DeviceBuffer.zeroed(s, 1, np.uint32)
+    for scale, asc_v in ((8e-3, 0.05), (1e-5, 1e-4), (3e-3, 0.02), (2e-6, 1e-5)):
+        ws = (rng.random(n) * scale + scale * 0.1).astype(F32)
+        asc = np.array([asc_v], F32)
+        want, _ = oracle.linear_argmax(q, asc, w, ws, k)
+        mod.linear_argmax(s, dq, dev(s, asc), dw, dev(s, ws), k, tok)
+        assert int(tok.to_host_vec(s)[0]) == want, (scale, asc_v)
+
+
 # ------------------------------------------------------------------ graphs
 def test_graph_replay_matches_eager(env):
     """Quantize -> linear -> fused lm_head argmax captured once and replayed
