@@ -47,6 +47,54 @@ def gemv_bytes(n: int, k: int, m: int = 1, out_bytes: int = 2) -> int:
     return n * k + 4 * n + m * k + 4 * m + out_bytes * m * n
 
 
+def measured_traffic():
+    """HBM bytes per gate_up launch from the committed FETCH_SIZE/WRITE_SIZE
+    profile (profiles/gemv_m1_gate_up_traffic.txt), or None."""
+    f = ROOT / "profiles" / "gemv_m1_gate_up_traffic.txt"
+    try:
+        for line in f.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def traffic_run() -> int:
+    """Workload for the counter passes: 36 gate_up GEMVs (distinct weights),
+    three times, eager launches; then a 256 MiB device copy three times as the
+    calibration kernel of known traffic (reads and writes 256 MiB)."""
+    from inferrous_amd import CudaContext, DeviceBuffer, load, synth
+    from inferrous_amd import _lib
+    ctx = CudaContext(0)
+    mod = load(ctx)
+    s = ctx.new_stream()
+    n, k = 24576, 4096
+    ws_ = []
+    for layer in range(synth.LAYERS):
+        w = DeviceBuffer.zeroed(s, n * k, np.int8)
+        sc = DeviceBuffer.zeroed(s, n, np.float32)
+        mod.synth_i8(s, w, SEED_W, synth.weight_stream(layer, 2))
+        mod.synth_f32(s, sc, SEED_S, synth.scale_stream(layer, 2), 1e-3, 1e-2)
+        ws_.append((w, sc))
+    x = DeviceBuffer.from_host(s, synth.normal_rows(40, 1, k).reshape(-1))
+    q = DeviceBuffer.zeroed(s, k, np.int8)
+    sc1 = DeviceBuffer.zeroed(s, 1, np.float32)
+    mod.quantize(s, None, x, k, q, sc1)
+    out = DeviceBuffer.zeroed(s, n, np.uint16)
+    for _ in range(3):
+        for (w, sc) in ws_:
+            mod.linear(s, None, q, sc1, w, sc, k, out)
+    s.synchronize()
+    src = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
+    dst = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
+    for _ in range(3):
+        _lib.check(_lib.lib().w8a8_memcpy_dtod(dst.ptr, src.ptr, 256 << 20, s.handle))
+    s.synchronize()
+    print("traffic run done", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -54,12 +102,17 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extras", action="store_true", help="headline + roofline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--traffic", action="store_true",
+                    help="run only the counter-profiling workload (gate_up GEMVs + calibration copy)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode in this "
               "build (the sharding design is described in DESIGN.md); run with --gpus 1.",
               file=sys.stderr)
         return 2
+
+    if args.traffic:
+        return traffic_run()
 
     from inferrous_amd import CudaContext, DeviceBuffer, Event, Graph, load, synth
 
@@ -167,27 +220,24 @@ def main() -> int:
     log(f"dispatch gap {gap_us:.2f} us/launch; in-kernel rate {in_kernel_gbs:.0f} GB/s")
 
     # ------------------------------------------------------------ roofline
-    # Dominant kernel: the K=4096 M=1 GEMV (gemv_m1, KC=4) that serves qkv, o
-    # and gate_up -- 108 of the 145 launches and ~75% of the step's bytes.
-    def k4096_chain():
-        for mats in layers:
-            for (name, n, k, w, ws) in mats:
-                if k == 4096:
-                    q, sc = qs[k]
-                    mod.linear(s, None, q, sc, w, ws, k, outs[name])
+    # Dominant kernel: gemv_m1<1,4,0>, the gate_up GEMV (24576 x 4096, one row
+    # per wave) -- the largest share of the step.  Timed as a graph of the 36
+    # distinct-weight launches of one token, HIP events on the launch stream.
+    gu = [mats[2] for mats in layers]
+    gu_bytes = gemv_bytes(24576, 4096)
 
-    g_dom = capture(k4096_chain)
-    dom_launches = 3 * synth.LAYERS
-    dom_bytes = sum(gemv_bytes(n, k) for (_, n, k, _, _) in layers[0] if k == 4096) * synth.LAYERS
-    dom_ms = time_graph(g_dom, max(10, args.steps // 2))
-    dom_avg_us = dom_ms * 1e3 / dom_launches
-    dom_gbs = dom_bytes / (dom_ms * 1e-3) / 1e9
-    roofline = {"kernel": "gemv_m1 K=4096 (R=2: qkv/o, R=1: gate_up)", "bound": "hbm",
+    def gate_up_chain():
+        for (name, n, k, w, ws) in gu:
+            mod.linear(s, None, qs[k][0], qs[k][1], w, ws, k, outs[name])
+
+    dom_ms = time_graph(capture(gate_up_chain), max(10, args.steps // 2))
+    dom_avg_us = dom_ms * 1e3 / len(gu)
+    dom_gbs = gu_bytes / (dom_avg_us * 1e-6) / 1e9
+    roofline = {"kernel": "gemv_m1<1,4,0> (gate_up 24576x4096, M=1)", "bound": "hbm",
                 "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                "avg_launch_us": round(dom_avg_us, 3),
-                "bytes_per_launch": dom_bytes // dom_launches}
-    log(f"dominant GEMV: {dom_avg_us:.2f} us/launch avg, {dom_gbs:.0f} GB/s")
+                "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "avg_launch_us": round(dom_avg_us, 3), "bytes_per_launch": gu_bytes}
+    log(f"dominant GEMV (gate_up): {dom_avg_us:.2f} us/launch avg, {dom_gbs:.0f} GB/s")
 
     result = {
         "metric": "decode GEMV HBM GB/s (% peak) at M=1; prefill INT8 TOPS (% peak) at M=512",
