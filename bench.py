@@ -106,8 +106,8 @@ def main() -> int:
                     help="run only the counter-profiling workload (gate_up GEMVs + calibration copy)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode in this "
-              "build (the sharding design is described in DESIGN.md); run with --gpus 1.",
+        print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode "
+              "(column/row/vocab sharding is a design note, not built); run with --gpus 1.",
               file=sys.stderr)
         return 2
 
