@@ -158,6 +158,30 @@ int w8a8_linear_grouped(void *stream, const int8_t *q, const float *asc,
                         const int8_t *const *w, const float *const *ws,
                         const size_t *n, void *const *out, int out_dtype);
 
+/* `linear_swiglu` (src/kernels.rs:619-695): gate and up projections of the
+ * same activations (each exactly as w8a8_linear) and
+ *   act = bf16(RN(RN(gate / RN(1 + exp(-gate))) * up))      (src/kernels.rs:681)
+ * gate, up, act are [m, n] in out_dtype (F32 or BF16).  If maxima != NULL,
+ * each row r's largest bits(|act|) (NaN -> 0) is folded into maxima[r] with
+ * atomicMax (the producer half of the `quantize_with_max` protocol,
+ * src/kernels.rs:133-147, :684-694); the caller resets maxima beforehand
+ * (w8a8_quantize's maxima_reset writes the 1e-8 floor).  The reference
+ * kernel is M = 1 only; larger m runs the two projections and w8a8_swiglu.
+ * exp is the device library's expf: act is tolerance-checked against the
+ * reference (its exp is an approximate exp2); gate, up and maxima-of-act are
+ * exact functions of their inputs. */
+int w8a8_linear_swiglu(void *stream, const int8_t *q, const float *asc,
+                       size_t m, uint32_t k, const int8_t *w_gate,
+                       const float *ws_gate, const int8_t *w_up,
+                       const float *ws_up, size_t n, void *gate, void *up,
+                       void *act, uint32_t *maxima, int out_dtype);
+
+/* `swiglu` (src/kernels.rs:2172-2190): act = as above, elementwise over
+ * gate/up [rows, width] in dtype (F32 or BF16); maxima as above, per row
+ * (the reference publishes only for its single 12288-wide decode row). */
+int w8a8_swiglu(void *stream, const void *gate, const void *up, size_t rows,
+                uint32_t width, void *act, uint32_t *maxima, int dtype);
+
 /* Greedy selection (`select_token`, src/kernels.rs:2191-2231): the largest
  * value, lowest index on ties (-0 == +0); empty input or any non-finite
  * value gives 0xFFFFFFFF.  Multi-workgroup: needs a device workspace of at

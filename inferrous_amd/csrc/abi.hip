@@ -413,6 +413,58 @@ int w8a8_linear_grouped(void* stream, const int8_t* q, const float* asc, size_t 
   return W8A8_OK;
 }
 
+int w8a8_swiglu(void* stream, const void* gate, const void* up, size_t rows, uint32_t width,
+                void* act, uint32_t* maxima, int dtype) {
+  if (dtype != W8A8_OUT_F32 && dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  if (rows == 0 || width == 0) return W8A8_OK;
+  if (!gate || !up || !act) return W8A8_ENULL;
+  if (rows > SIZE_MAX / width) return W8A8_ESHAPE;
+  const size_t a = out_align(dtype);
+  if (!al(gate, a) || !al(up, a) || !al(act, a) || !al(maxima, 4)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_swiglu((hipStream_t)stream, gate, up, rows, width, act, dtype, maxima));
+}
+
+int w8a8_linear_swiglu(void* stream, const int8_t* q, const float* asc, size_t m, uint32_t k,
+                       const int8_t* w_gate, const float* ws_gate, const int8_t* w_up,
+                       const float* ws_up, size_t n, void* gate, void* up, void* act,
+                       uint32_t* maxima, int out_dtype) {
+  if (out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  int s = check_linear(q, asc, m, w_gate, ws_gate, n, k, gate, out_dtype);
+  if (s != W8A8_OK) return s;
+  s = check_linear(q, asc, m, w_up, ws_up, n, k, up, out_dtype);
+  if (s != W8A8_OK) return s;
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (!act) return W8A8_ENULL;
+  if (!al(act, out_align(out_dtype)) || !al(maxima, 4)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  hipStream_t st = (hipStream_t)stream;
+  if (m == 1 && (k == 4096 || k == 12288)) {
+    SwigluArgs a{};
+    a.q = q;
+    a.asc = asc;
+    a.k = k;
+    a.n = (uint32_t)n;
+    a.wg = w_gate;
+    a.wsg = ws_gate;
+    a.wu = w_up;
+    a.wsu = ws_up;
+    a.gate = gate;
+    a.up = up;
+    a.act = act;
+    a.out_dtype = out_dtype;
+    a.maxima = maxima;
+    return hip_status(launch_gemv_swiglu(st, a));
+  }
+  const int8_t* w[2] = {w_gate, w_up};
+  const float* ws[2] = {ws_gate, ws_up};
+  const size_t nn[2] = {n, n};
+  void* out[2] = {gate, up};
+  s = w8a8_linear_grouped(stream, q, asc, m, k, 2, w, ws, nn, out, out_dtype);
+  if (s != W8A8_OK) return s;
+  return hip_status(launch_swiglu(st, gate, up, m, (uint32_t)n, act, out_dtype, maxima));
+}
+
 size_t w8a8_select_workspace_bytes(size_t n) {
   (void)n;
   return kSelectSlots * kSelectStride * sizeof(uint64_t);

@@ -44,6 +44,16 @@ __device__ __forceinline__ float dequant(int32_t acc, float asc, float ws) {
   return bf16_rne(t * ws);
 }
 
+// SiLU(g) * u in the reference's operation order (src/kernels.rs:681,
+// :2181): bf(RN(RN(g / RN(1 + exp(-g))) * u)).  exp is the ROCm device
+// library's expf (accurate to about 1 ulp); the reference uses an
+// approximate exp2, so this one value is tolerance-checked, not bit-exact.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float d = 1.0f + expf(-g);
+  const float s = g / d;
+  return bf16_rne(s * u);
+}
+
 __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }

@@ -25,6 +25,8 @@
 // INT32 sums are exact (|acc| <= 12288 * 127^2 < 2^31), so the lane/chunk
 // order is free; the epilogue keeps the reference's two RN multiplies and
 // BF16 RNE (device_common.hpp `dequant`).
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -237,6 +239,93 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
   if (EPI == EPI_ARGMAX && writer) select_publish_lane(select_key(value, row), row, a.slots);
 }
 
+// Producer side of the maxima protocol (publish_absmax, src/kernels.rs:133-147):
+// the workgroup's largest bits(|v|) (NaN -> 0) is folded into *p with one
+// atomicMax.  *p only grows while producers run, so the thread first reads
+// it (device-coherent relaxed load) and skips the atomic when not larger.
+// Every thread of the workgroup must call this (it has a barrier).
+__device__ __forceinline__ void publish_absmax_block(uint32_t bits, uint32_t* p) {
+  __shared__ uint32_t wmax[kGemvWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  bits = wave_max_u32(bits);
+  if (lane == 0) wmax[wave] = bits;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t b = wmax[0];
+#pragma unroll
+    for (int i = 1; i < kGemvWaves; ++i) b = wmax[i] > b ? wmax[i] : b;
+    if (b > __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(p, b);
+  }
+}
+
+// linear_swiglu (src/kernels.rs:619-695) at M = 1: one wave owns output
+// coordinate c and streams gate row c and up row c (2 x k bytes) against the
+// activation row held in registers; lane 0 writes gate, up (bit-exact
+// linear epilogues) and act = silu_mul(gate, up), then the workgroup
+// publishes its largest |act| into maxima[0].
+template <int KC>
+__global__ __launch_bounds__(kGemvThreads) void gemv_swiglu(SwigluArgs a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t c = blockIdx.x * kGemvWaves + wave_id();
+  const bool live = c < a.n;
+  constexpr uint32_t K = KC * 1024;
+  int ag = 0, au = 0;
+  if (live) {
+    v4i x[KC], wg[KC], wu[KC];
+#pragma unroll
+    for (int i = 0; i < KC; ++i) x[i] = load16(a.q + i * 1024 + lane * 16);
+    const int8_t* pg = a.wg + (size_t)c * K + lane * 16;
+    const int8_t* pu = a.wu + (size_t)c * K + lane * 16;
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      wg[i] = load_nt16(pg + i * 1024);
+      wu[i] = load_nt16(pu + i * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      ag = dot16(x[i], wg[i], ag);
+      au = dot16(x[i], wu[i], au);
+    }
+  }
+  const int tg = wave_sum_uniform(ag);
+  const int tu = wave_sum_uniform(au);
+  uint32_t bits = 0;
+  if (live && lane == 0) {
+    const float g = dequant(tg, a.asc[0], a.wsg[c]);
+    const float u = dequant(tu, a.asc[0], a.wsu[c]);
+    const float v = silu_mul(g, u);
+    store_out(a.gate, c, a.out_dtype, tg, g);
+    store_out(a.up, c, a.out_dtype, tu, u);
+    store_out(a.act, c, a.out_dtype, 0, v);
+    bits = abs_bits_no_nan(v);
+  }
+  if (a.maxima) publish_absmax_block(bits, a.maxima);
+}
+
+__device__ __forceinline__ float load_val(const void* p, size_t i, int dtype) {
+  if (dtype == W8A8_OUT_BF16)
+    return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
+  return reinterpret_cast<const float*>(p)[i];
+}
+
+// swiglu (src/kernels.rs:2172-2190): act = silu_mul(gate, up) elementwise
+// over rows x width (blockIdx.y = row); with maxima, each row's largest
+// |act| is published into maxima[row].
+__global__ __launch_bounds__(kGemvThreads) void swiglu_kernel(const void* gate, const void* up,
+                                                               uint32_t width, void* act, int dtype,
+                                                               uint32_t* maxima) {
+  const size_t r = blockIdx.y;
+  uint32_t bits = 0;
+  for (uint32_t j = blockIdx.x * kGemvThreads + threadIdx.x; j < width;
+       j += gridDim.x * kGemvThreads) {
+    const size_t i = r * width + j;
+    const float v = silu_mul(load_val(gate, i, dtype), load_val(up, i, dtype));
+    store_out(act, i, dtype, 0, v);
+    bits = max(bits, abs_bits_no_nan(v));
+  }
+  if (maxima) publish_absmax_block(bits, maxima + r);
+}
+
 // Standalone greedy selection over f32 values.
 __global__ __launch_bounds__(kGemvThreads) void select_kernel(const float* __restrict__ x, size_t n,
                                                                uint64_t* slots) {
@@ -318,6 +407,35 @@ hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kSelectSlots), 0, st, a.slots, a.token);
   return hipGetLastError();
+}
+
+hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {
+  if (a.n == 0) return hipSuccess;
+  const dim3 grid((a.n + kGemvWaves - 1) / kGemvWaves);
+  if (a.k == 4096)
+    hipLaunchKernelGGL(gemv_swiglu<4>, grid, dim3(kGemvThreads), 0, st, a);
+  else if (a.k == 12288)
+    hipLaunchKernelGGL(gemv_swiglu<12>, grid, dim3(kGemvThreads), 0, st, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_t rows,
+                         uint32_t width, void* act, int dtype, uint32_t* maxima) {
+  if (rows == 0 || width == 0) return hipSuccess;
+  const uint32_t bx = std::min<uint32_t>((width + kGemvThreads - 1) / kGemvThreads, 64u);
+  const size_t esz = dtype == W8A8_OUT_BF16 ? 2 : 4;
+  for (size_t r0 = 0; r0 < rows; r0 += 65535) {
+    const uint32_t ry = (uint32_t)std::min<size_t>(rows - r0, 65535);
+    const size_t off = r0 * width * esz;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(bx, ry), dim3(kGemvThreads), 0, st,
+                       (const char*)gate + off, (const char*)up + off, width, (char*)act + off,
+                       dtype, maxima ? maxima + r0 : nullptr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* slots, uint32_t* token) {

@@ -31,6 +31,22 @@ struct GemvArgs {
   uint32_t* token;
 };
 
+// Fused gate/up GEMV with the SiLU product (M = 1).
+struct SwigluArgs {
+  const int8_t* q;
+  const float* asc;
+  uint32_t k, n;
+  const int8_t* wg;
+  const float* wsg;
+  const int8_t* wu;
+  const float* wsu;
+  void* gate;
+  void* up;
+  void* act;
+  int out_dtype;      // F32 or BF16
+  uint32_t* maxima;   // optional: atomicMax of bits(|act|)
+};
+
 struct GemmArgs {
   const int8_t* q;
   const float* asc;
@@ -52,6 +68,9 @@ hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);
+hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a);  // m == 1, k in {4096, 12288}
+hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_t rows,
+                         uint32_t width, void* act, int dtype, uint32_t* maxima);
 hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* slots, uint32_t* token);
 
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a);

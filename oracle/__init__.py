@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
             "orc_epilogue": (None, [P, P, S, P, S, P, P]),
             "orc_linear": (None, [P, P, S, P, P, S, S, P, P, P, ctypes.c_int]),
             "orc_residual": (None, [P, P, S, P]),
+            "orc_silu_mul": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+            "orc_swiglu": (ctypes.c_uint32, [P, P, S, P]),
             "orc_argmax": (ctypes.c_uint32, [P, S]),
             "orc_linear_argmax": (ctypes.c_uint32, [P, P, P, P, S, S, P, ctypes.c_int]),
             "orc_mix64": (U64, [U64]),
@@ -176,6 +178,15 @@ def residual(res, out):
     comb = np.empty(res.size, np.float32)
     lib().orc_residual(_p(res), _p(out), res.size, _p(comb))
     return comb
+
+
+def swiglu(gate, up):
+    """(act f32[n], published maximum bits) -- src/kernels.rs:2172-2190."""
+    g = _c(gate, np.float32).reshape(-1)
+    u = _c(up, np.float32).reshape(-1)
+    act = np.empty(g.size, np.float32)
+    mx = int(lib().orc_swiglu(_p(g), _p(u), g.size, _p(act)))
+    return act, mx
 
 
 def argmax(x) -> int:

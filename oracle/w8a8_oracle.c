@@ -189,6 +189,17 @@ void orc_residual(const float *residual, const float *out, size_t n,
   for (size_t i = 0; i < n; ++i) combined[i] = orc_bf16_rne(residual[i] + out[i]);
 }
 
+float orc_silu_mul(float g, float u) {
+  float d = 1.0f + expf(-g); /* RN add (built with -ffp-contract=off) */
+  float s = g / d;           /* RN division */
+  return orc_bf16_rne(s * u);
+}
+
+uint32_t orc_swiglu(const float *gate, const float *up, size_t n, float *act) {
+  for (size_t i = 0; i < n; ++i) act[i] = orc_silu_mul(gate[i], up[i]);
+  return orc_absmax_bits(act, n); /* fold(1e-8, max |act|), NaN ignored */
+}
+
 /* src/kernels.rs:2196-2229: scan with (v > best) || (v == best && i < idx);
  * a sequential ascending scan with strict '>' keeps the lowest index, and
  * IEEE '==' makes -0 and +0 tie (src/model.rs:210-215). */

@@ -69,6 +69,17 @@ void orc_linear(const int8_t *q, const float *asc, size_t m, const int8_t *w,
 void orc_residual(const float *residual, const float *out, size_t n,
                   float *combined);
 
+/* SiLU product of src/kernels.rs:681 / :2181:
+ * bf(RN(RN(g / RN(1 + exp(-g))) * u)), with exp = C99 expf.  The
+ * reference's exp is an approximate exp2 (src/kernels.rs:21-23) that is
+ * not reproduced, so results are compared within the reference's own
+ * tolerance (src/conformance.rs:663: |a-b| <= 2e-4 + 0.01|b|). */
+float orc_silu_mul(float g, float u);
+/* src/kernels.rs:2172-2190 `swiglu` over n elements; returns the
+ * published maximum fold(1e-8, max |act|) as f32 bits
+ * (src/conformance.rs:596-603). */
+uint32_t orc_swiglu(const float *gate, const float *up, size_t n, float *act);
+
 /* src/kernels.rs:2191-2231 `select_token` (equal to src/model.rs:206-218
  * `argmax` when that returns Ok): largest value, lowest index on ties,
  * -0 == +0; empty input or any non-finite value -> 0xFFFFFFFF. */

@@ -103,3 +103,22 @@ def argmax_expected(x: np.ndarray) -> int:
         if x[i] > x[best]:
             best = i
     return best
+
+
+def reference_tolerance_ok(got, want) -> bool:
+    """The reference's tolerance for non-exact operators
+    (src/conformance.rs:660-673): every element finite with
+    |a-b| <= 2e-4 + 0.01|b|, and relative L2 error <= 0.005."""
+    got = np.asarray(got, np.float64).reshape(-1)
+    want = np.asarray(want, np.float64).reshape(-1)
+    elem = bool(np.isfinite(got).all()) and bool(
+        np.all(np.abs(got - want) <= 2e-4 + 0.01 * np.abs(want)))
+    l2 = np.sqrt(np.sum((got - want) ** 2) / max(float(np.sum(want ** 2)), 1e-20))
+    return elem and l2 <= 0.005
+
+
+def bf16_ulp_distance(a, b) -> np.ndarray:
+    """|a - b| in BF16 ulps for BF16-valued f32 arrays of the same sign."""
+    ia = (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.int64)
+    ib = (np.ascontiguousarray(b, np.float32).view(np.uint32) >> 16).astype(np.int64)
+    return np.abs(ia - ib)

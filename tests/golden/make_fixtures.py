@@ -14,6 +14,12 @@ generator (bitemyapp/inferrous, crates/inferrous-qwen3/tools/operator_fixtures.p
   weight rows 0/1 all +127/-127 (worst accumulator +-198,193,152 at 12288),
   ``asc ~ U[0, 1/64)``, ``ws ~ U[0, 1/64)``,
   expected ``out = bf16((q @ w.T).float() * asc * ws)``.
+* swiglu (tools/operator_fixtures.py:75-76): gate = bf16(linspace(-80, 80,
+  12288)), up = bf16(randn(12288)), expected ``out = bf16(silu(gate) * up)``
+  in torch's float32 (compared within the reference's tolerance,
+  src/conformance.rs:663).  The reference draws its rope/attention inputs
+  before this case; those draws are not repeated, so ``up`` differs from the
+  reference's own file while following the same recipe.
 
 Expected values are computed here with torch on the CPU -- an implementation
 independent of the C oracle in oracle/ -- and stored with the inputs.  The
@@ -90,6 +96,11 @@ def main() -> None:
         res = to_bf16_values(acc.to(torch.float32) * asc * ws)
         out.add("linear", {"q": q, "asc": asc, "w": w, "ws": ws, "acc": acc,
                            "out": res}, width=width)
+
+    gate = to_bf16_values(torch.linspace(-80, 80, 12288))
+    up = to_bf16_values(torch.randn(12288))
+    act = to_bf16_values(torch.nn.functional.silu(gate) * up)
+    out.add("swiglu", {"gate": gate, "up": up, "out": act})
 
     manifest = {"generator": "tests/golden/make_fixtures.py", "torch": torch.__version__,
                 "seed": 824, "cases": out.cases}

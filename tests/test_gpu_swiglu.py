@@ -1,0 +1,217 @@
+"""GPU parity of the SwiGLU producers: `linear_swiglu` (src/kernels.rs:619-695)
+and `swiglu` (src/kernels.rs:2172-2190), and the decode MLP chain they feed
+(src/gpu.rs:713-790: norm-quantize reset -> linear_swiglu -> quantize_with_max
+-> linear_residual).
+
+gate and up are linear epilogues: bit-exact against the oracle.  act uses an
+exponential the reference computes with an approximate exp2; it is checked
+against the oracle within the reference's own tolerance
+(src/conformance.rs:663, |a-b| <= 2e-4 + 0.01|b|, relative L2 <= 0.005) and,
+tighter, within one BF16 ulp.  Like the reference's test
+(src/conformance.rs:741-838), the fused kernel must equal the separate
+projections + swiglu bit for bit, and the published maximum must equal
+fold(1e-8, max |act|) of the values actually written.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import bf16_ulp_distance, reference_tolerance_ok
+from inferrous_amd import CudaContext, DeviceBuffer, Graph, load, rows
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+FLOOR = int(np.array([1e-8], F32).view(np.uint32)[0])
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def env():
+    ctx = CudaContext(0)
+    stream = ctx.new_stream()
+    return ctx, load(ctx), stream
+
+
+def dev(stream, a):
+    return DeviceBuffer.from_host(stream, np.ascontiguousarray(a))
+
+
+def fold_max(act) -> int:
+    a = np.abs(np.asarray(act, F32).reshape(-1))
+    a = a[~np.isnan(a)]
+    return int(max(FLOOR, int(bits(a).max()) if a.size else 0))
+
+
+def act_close(got, gate, up):
+    want, _ = oracle.swiglu(gate, up)
+    assert reference_tolerance_ok(got, want)
+    same = (np.sign(got) == np.sign(want)) & (want != 0)
+    assert bf16_ulp_distance(got[same], want[same]).max(initial=0) <= 1
+
+
+def deterministic_inputs(k, n):
+    """src/conformance.rs:746-777."""
+    i = np.arange(k, dtype=np.int64)
+    q = ((i * 13 % 255) - 127).astype(np.int8)
+    j = np.arange(k * n, dtype=np.int64)
+    w0 = ((j * 31 % 255) - 127).astype(np.int8)
+    w1 = ((j * 17 % 251) - 125).astype(np.int8)
+    asc = np.array([0.002], F32)
+    c = np.arange(n)
+    s0 = (F32(0.0001) * ((c % 7) + 1).astype(F32)).astype(F32)
+    s1 = (F32(0.0001) * ((c % 11) + 1).astype(F32)).astype(F32)
+    return q, asc, w0, s0, w1, s1
+
+
+@pytest.mark.parametrize("k,n", [(128, 33), (4096, 12288), (12288, 33), (4096, 4099)])
+def test_fused_gate_up_matches_separate(env, k, n):
+    ctx, mod, s = env
+    print(f"linear_swiglu k={k} n={n}", flush=True)
+    q, asc, w0, s0, w1, s1 = deterministic_inputs(k, n)
+    dq, da = dev(s, q), dev(s, asc)
+    dw0, ds0, dw1, ds1 = dev(s, w0), dev(s, s0), dev(s, w1), dev(s, s1)
+    z = lambda: DeviceBuffer.zeroed(s, n, np.float32)  # noqa: E731
+    g, u, act = z(), z(), z()
+    maximum = dev(s, np.array([FLOOR], np.uint32))
+    mod.linear_pair(s, None, dq, da, k, dw0, ds0, g, dw1, ds1, u)
+    mod.swiglu(s, None, g, u, act, maximum)
+    exp_g, exp_u, exp_act = (b.to_host_vec(s) for b in (g, u, act))
+    exp_max = fold_max(exp_act)
+    if n == 12288:   # the reference's swiglu publishes only for the decode row
+        assert int(maximum.to_host_vec(s)[0]) == exp_max
+    else:
+        assert int(maximum.to_host_vec(s)[0]) == FLOOR
+
+    g2, u2, act2 = z(), z(), z()
+    maximum.copy_from_host(s, np.array([FLOOR], np.uint32))
+    mod.linear_swiglu(s, rows((n + 7) // 8, 256), dq, da, k, dw0, ds0, g2, dw1, ds1, u2, act2,
+                      maximum)
+    assert np.array_equal(bits(g2.to_host_vec(s)), bits(exp_g)), "gate bits"
+    assert np.array_equal(bits(u2.to_host_vec(s)), bits(exp_u)), "up bits"
+    assert np.array_equal(bits(act2.to_host_vec(s)), bits(exp_act)), "activation bits"
+    assert int(maximum.to_host_vec(s)[0]) == exp_max, "activation maximum"
+
+    _, og, _ = oracle.linear(q, asc, w0, s0, k)
+    _, ou, _ = oracle.linear(q, asc, w1, s1, k)
+    assert np.array_equal(bits(exp_g), bits(og))
+    assert np.array_equal(bits(exp_u), bits(ou))
+    act_close(exp_act, og, ou)
+
+
+def test_swiglu_fixture(env, fixtures):
+    ctx, mod, s = env
+    (case,) = fixtures.cases("swiglu")
+    g, u, want = (fixtures.tensor(case, key) for key in ("gate", "up", "out"))
+    out = DeviceBuffer.zeroed(s, g.size, np.float32)
+    maxima = dev(s, np.array([FLOOR], np.uint32))
+    mod.swiglu(s, None, dev(s, g), dev(s, u), out, maxima)
+    got = out.to_host_vec(s)
+    assert reference_tolerance_ok(got, want)
+    act_close(got, g, u)
+    assert int(maxima.to_host_vec(s)[0]) == fold_max(got)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1024, 300), (2, 4096, 12288), (4, 4096, 12288),
+                                   (17, 4096, 1000), (129, 4096, 12288)])
+@pytest.mark.parametrize("dtype", [np.float32, np.uint16])
+def test_linear_swiglu_rows(env, m, k, n, dtype):
+    """Any M (the reference kernel is M = 1 only): per-row maxima, BF16 and
+    f32 outputs, both GEMV and MFMA families underneath."""
+    ctx, mod, s = env
+    print(f"linear_swiglu m={m} k={k} n={n} dtype={np.dtype(dtype).name}", flush=True)
+    rng = np.random.default_rng(m * 7 + k + n)
+    q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    asc = (rng.random(m) / 512 + 1e-4).astype(F32)
+    w0 = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    w1 = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    s0 = (rng.random(n) / 256 + 1e-4).astype(F32)
+    s1 = (rng.random(n) / 256 + 1e-4).astype(F32)
+    z = lambda: DeviceBuffer.zeroed(s, m * n, dtype)  # noqa: E731
+    g, u, act = z(), z(), z()
+    maxima = dev(s, np.full(m, FLOOR, np.uint32))
+    mod.linear_swiglu(s, None, dev(s, q), dev(s, asc), k, dev(s, w0), dev(s, s0), g, dev(s, w1),
+                      dev(s, s1), u, act, maxima)
+
+    def host(b):
+        v = b.to_host_vec(s)
+        return (v.astype(np.uint32) << 16).view(F32) if dtype == np.uint16 else v
+
+    _, og, _ = oracle.linear(q, asc, w0, s0, k, threads=8)
+    _, ou, _ = oracle.linear(q, asc, w1, s1, k, threads=8)
+    hg, hu, ha = host(g), host(u), host(act)
+    assert np.array_equal(bits(hg), bits(og))
+    assert np.array_equal(bits(hu), bits(ou))
+    act_close(ha, og, ou)
+    mx = maxima.to_host_vec(s)
+    for r in range(m):
+        assert int(mx[r]) == fold_max(ha.reshape(m, n)[r]), f"row {r}"
+
+
+def test_decode_mlp_chain_and_graph_replay(env):
+    """src/gpu.rs:713-790 at decode shapes: the norm quantize resets maxima,
+    linear_swiglu publishes max |act|, quantize_with_max (K=12288) uses it,
+    linear_residual (down) closes the block.  Replayed from a graph three
+    times with eager work in between; each replay equals the eager pass."""
+    ctx, mod, s = env
+    rng = np.random.default_rng(2024)
+    h, f = 4096, 12288
+    x = oracle.bf16_rne(rng.standard_normal(h).astype(F32))
+    res = oracle.bf16_rne(rng.standard_normal(h).astype(F32))
+    wg = rng.integers(-127, 128, (f, h), dtype=np.int8)
+    wu = rng.integers(-127, 128, (f, h), dtype=np.int8)
+    wd = rng.integers(-127, 128, (h, f), dtype=np.int8)
+    sg, su = (rng.random(f) / 4096 + 1e-5).astype(F32), (rng.random(f) / 4096 + 1e-5).astype(F32)
+    sd = (rng.random(h) / 4096 + 1e-5).astype(F32)
+    dx, dres = dev(s, x), dev(s, res)
+    dwg, dwu, dwd = dev(s, wg), dev(s, wu), dev(s, wd)
+    dsg, dsu, dsd = dev(s, sg), dev(s, su), dev(s, sd)
+    q4, q12 = DeviceBuffer.zeroed(s, h, np.int8), DeviceBuffer.zeroed(s, f, np.int8)
+    sc4, sc12 = DeviceBuffer.zeroed(s, 1, np.float32), DeviceBuffer.zeroed(s, 1, np.float32)
+    maxima = DeviceBuffer.zeroed(s, 1, np.uint32)
+    g, u, act = (DeviceBuffer.zeroed(s, f, np.float32) for _ in range(3))
+    down, hidden = DeviceBuffer.zeroed(s, h, np.float32), DeviceBuffer.zeroed(s, h, np.float32)
+
+    def block():
+        mod.quantize(s, None, dx, h, q4, sc4, maxima_reset=maxima)
+        mod.linear_swiglu(s, None, q4, sc4, h, dwg, dsg, g, dwu, dsu, u, act, maxima)
+        mod.quantize_with_max(s, None, act, f, maxima, q12, sc12)
+        mod.linear_residual(s, None, q12, sc12, dwd, dsd, f, dres, down, hidden)
+
+    block()
+    eager = {name: b.to_host_vec(s).copy() for name, b in
+             (("act", act), ("q12", q12), ("sc12", sc12), ("max", maxima), ("hidden", hidden))}
+
+    # oracle chain on the same inputs; act comes from the GPU (tolerance op)
+    oq4, osc4 = oracle.quantize(x, h)
+    _, og, _ = oracle.linear(oq4, osc4, wg, sg, h, threads=8)
+    _, ou, _ = oracle.linear(oq4, osc4, wu, su, h, threads=8)
+    assert np.array_equal(bits(g.to_host_vec(s)), bits(og))
+    assert np.array_equal(bits(u.to_host_vec(s)), bits(ou))
+    act_close(eager["act"], og, ou)
+    assert int(eager["max"][0]) == oracle.absmax_bits(eager["act"])
+    oq12, osc12 = oracle.quantize(eager["act"], f)
+    assert np.array_equal(eager["q12"], oq12)
+    assert np.array_equal(bits(eager["sc12"]), bits(osc12))
+    _, od, _ = oracle.linear(oq12, osc12, wd, sd, f, threads=8)
+    assert np.array_equal(bits(eager["hidden"]), bits(oracle.residual(res, od)))
+
+    graph = Graph(s)
+    with graph:
+        block()
+    for rep in range(3):
+        for b in (act, q12, hidden):
+            b.fill_zero(s)
+        maxima.copy_from_host(s, np.array([0xFFFFFFFF >> 1], np.uint32))  # stale large value
+        s.synchronize()
+        graph.launch()
+        s.synchronize()
+        for name, b in (("act", act), ("q12", q12), ("sc12", sc12), ("max", maxima),
+                        ("hidden", hidden)):
+            assert np.array_equal(b.to_host_vec(s).view(np.uint8), eager[name].view(np.uint8)), \
+                f"replay {rep}: {name}"

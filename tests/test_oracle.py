@@ -13,8 +13,8 @@ import pytest
 import torch
 
 import oracle
-from conftest import (argmax_cases, argmax_expected, rounding_expected,
-                      rounding_probe_inputs)
+from conftest import (argmax_cases, argmax_expected, bf16_ulp_distance,
+                      reference_tolerance_ok, rounding_expected, rounding_probe_inputs)
 
 F32 = np.float32
 
@@ -161,6 +161,50 @@ def test_residual_closed_form():
     res = ((np.arange(4096) % 17).astype(F32) - 8) * F32(0.0625)   # src/conformance.rs:236-241
     want = torch.from_numpy((res + out).astype(F32)).bfloat16().float().numpy()
     assert np.array_equal(bits(oracle.residual(res, out)), bits(want))
+
+
+# --------------------------------------------------------------- swiglu
+def test_swiglu_matches_fixture_within_reference_tolerance(fixtures):
+    (case,) = fixtures.cases("swiglu")
+    g, u = fixtures.tensor(case, "gate"), fixtures.tensor(case, "up")
+    want = fixtures.tensor(case, "out")
+    act, mx = oracle.swiglu(g, u)
+    assert reference_tolerance_ok(act, want)
+    # torch evaluates silu as x * sigmoid(x): a different rounding order, so
+    # values may differ by one BF16 ulp, never more.
+    same_sign = np.sign(act) == np.sign(want)
+    assert bf16_ulp_distance(act[same_sign], want[same_sign]).max() <= 1
+    assert mx == int(bits(np.maximum(np.abs(act).max(), F32(1e-8)))[0])
+
+
+def test_silu_mul_against_float64_and_closed_forms():
+    rng = np.random.default_rng(11)
+    g = oracle.bf16_rne(rng.uniform(-90, 90, 200_000).astype(F32))
+    u = oracle.bf16_rne(rng.standard_normal(200_000).astype(F32))
+    act, _ = oracle.swiglu(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    exact = g64 / (1.0 + np.exp(-g64)) * u64
+    want = oracle.bf16_rne(exact.astype(F32))
+    assert reference_tolerance_ok(act, want)
+    nz = (want != 0) & (np.sign(act) == np.sign(want))
+    d = bf16_ulp_distance(act[nz], want[nz])
+    assert d.max() <= 1 and np.mean(d) < 0.01
+    # closed forms: silu(0) = 0; silu(g) = g for large g; silu(g) -> 0- for very negative g
+    assert oracle.lib().orc_silu_mul(0.0, 3.0) == 0.0
+    assert oracle.lib().orc_silu_mul(100.0, 1.5) == 150.0
+    assert abs(oracle.lib().orc_silu_mul(-100.0, 1.0)) < 1e-40
+    # a planted operand swap (silu(up) * gate) is far outside the tolerance
+    swapped, _ = oracle.swiglu(u, g)
+    assert not reference_tolerance_ok(swapped, want)
+
+
+def test_swiglu_maximum_ignores_nan_and_keeps_floor():
+    act, mx = oracle.swiglu(np.zeros(8, F32), np.ones(8, F32))
+    assert mx == int(bits(F32(1e-8))[0])
+    g = np.array([1.0, np.nan, -4.0], F32)
+    act, mx = oracle.swiglu(g, np.ones(3, F32))
+    assert np.isnan(act[1])
+    assert mx == int(bits(np.abs(act[[0, 2]]).max())[0])
 
 
 # --------------------------------------------------------------- argmax
