@@ -15,21 +15,20 @@
 // 4 x i32 result of lane l holds rows 4*(l/16)+v, column l%16.
 //
 // Three kernels:
-//  * gemm_dma (M > 64, k % 64 == 0): the prefill GEMM, built on
+//  * gemm_dma (M > 64, k % 128 == 0): the prefill GEMM, built on
 //    v_mfma_i32_32x32x32_i8 (on gfx950 the 16x16x64 int8 form issues at half
-//    its rate).  Operands move global -> LDS with global_load_lds_dwordx4
-//    (no VGPR staging) through an S-stage ring, one barrier per 64-byte K
-//    stage.  Each wave-wide DMA moves 16 rows x 64 bytes with four adjacent
-//    lanes per row (coalesced); the 16-byte chunk order inside each row is
-//    XOR-swizzled with g(r) = ((r >> 1) ^ (r >> 2)) & 3 so the MFMA fragment
-//    reads (row = lane % 32, chunk = 2s + lane / 32) are bank-conflict free.
-//    Workgroups are numbered XCD-aware (below).  Tile shape per problem is
-//    chosen by the host (measured: large N -> 256 x 192, else 64 x 128).
+//    its rate), eight waves per workgroup (two per SIMD, so one wave's LDS
+//    reads overlap the other's MFMAs).  Operands move global -> LDS with
+//    global_load_lds_dwordx4 (no VGPR staging) in 128-byte K stages (whole
+//    cache lines) through an S-stage ring, one barrier per stage; the
+//    16-byte chunks of each LDS row are XOR-swizzled so fragment reads are
+//    bank-conflict free.  Workgroups are numbered XCD-aware (below).  Tile
+//    shape per problem is chosen by the host from the tile count.
 //  * gemm_skinny (M <= 64, HBM-bound): one workgroup owns 16 weight rows;
 //    its S waves split K and stream their weight fragments straight from
 //    HBM into MFMA B operands (no LDS round trip), activation fragments come
 //    from L1/L2.  Partial i32 tiles are summed through LDS -- exact.
-//  * gemm_tiled (M > 64 with k % 64 != 0): BM x BN output tile, 4 waves, 128-byte K stages
+//  * gemm_tiled (M > 64 with k % 128 != 0): BM x BN output tile, 4 waves, 128-byte K stages
 //    double-buffered in LDS (row pitch 144 B: a 16-lane ds_read_b128 column
 //    touches every bank once), global loads of stage k+1 in flight while
 //    stage k feeds the MFMAs.  Workgroups are numbered so that the M tiles
@@ -229,7 +228,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-__device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
 #define W8A8_LDS_PTR(p) ((void __attribute__((address_space(3)))*)(p))
 
@@ -256,17 +254,27 @@ __device__ __forceinline__ void store_ep(const GemmArgs& a, uint32_t r, uint32_t
   }
 }
 
+// Prefill GEMM.  Workgroup = 8 waves (two per SIMD: while one wave waits on
+// LDS the other keeps the matrix core busy), output tile BM x BN, wave tile
+// WM x WN built from 32x32 MFMA blocks.  K advances in 128-byte stages, so
+// every DMA row request is one whole 128-byte cache line.  A stage holds BM
+// activation rows then BN weight rows, 128 bytes each; 16-byte chunk c of LDS
+// row r sits at chunk c ^ (r & 7), so the fragment reads of eight
+// consecutive rows hit eight different 16-byte bank groups.  Sub-step i of a
+// stage covers k bytes [32i, 32i + 32): lane l (row / column l % 32,
+// half h = l / 32) reads chunk 2i + h -- the same lane -> k map for A and B.
+// S stages form a ring; stage kt + S is loaded into stage kt's slot once
+// every wave has finished reading it (one barrier per stage).
 template <int BM, int BN, int WM, int WN, int S, int EP>
-__global__ __launch_bounds__(256) void gemm_dma(GemmArgs a, uint32_t tiles_m, uint32_t tiles_n) {
+__global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, uint32_t tiles_n) {
   constexpr int WAVES_N = BN / WN;
-  static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
-  static_assert(WM % 32 == 0 && WN % 32 == 0 && S >= 2 && S <= 6, "tile shape");
+  static_assert((BM / WM) * (BN / WN) == 8, "eight waves per workgroup");
+  static_assert(WM % 32 == 0 && WN % 32 == 0 && S >= 2 && S <= 4, "tile shape");
   constexpr int FM = WM / 32, FN = WN / 32;
-  constexpr int AB = BM / 16, BB = BN / 16;  // 1 KiB DMA blocks (16 rows x 64 B) per stage
-  constexpr int NB = AB + BB;
-  static_assert(NB % 4 == 0, "DMA blocks divide among the four waves");
-  constexpr int L = NB / 4;                  // DMA loads per wave per stage
-  constexpr int STAGE = NB * 1024;
+  constexpr int NR = BM + BN;    // LDS rows per stage
+  constexpr int STAGE = NR * 128;
+  static_assert(NR % 64 == 0, "1 KiB DMA blocks (8 rows) divide among the eight waves");
+  constexpr int L = NR / 64;     // DMA loads per wave per stage
   __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
 
   const uint32_t T = tiles_m * tiles_n;
@@ -276,69 +284,91 @@ __global__ __launch_bounds__(256) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
-  const uint32_t K = a.k, KT = K / 64;
+  const uint32_t K = a.k, KT = K / 128;
 
   // Sources of this wave's DMA blocks; rows past M / N re-read row 0 (their
   // products only reach accumulator cells that are never stored).
   const int8_t* src[L];
 #pragma unroll
   for (int j = 0; j < L; ++j) {
-    const int b = wave * L + j;
-    const int rr = lane >> 2, cc = (lane & 3) ^ lds_swizzle(rr);
-    const bool isA = b < AB;
-    const uint32_t row = (isA ? m0 + b * 16 : n0 + (b - AB) * 16) + rr;
+    const int row = 8 * (wave * L + j) + (lane >> 3);
+    const int gc = (lane & 7) ^ (row & 7);
+    const bool isA = row < BM;
+    const uint32_t g = isA ? m0 + row : n0 + (row - BM);
     const uint32_t lim = isA ? a.m : a.n;
-    src[j] = (isA ? a.q : a.w) + (size_t)(row < lim ? row : 0) * K + cc * 16;
+    src[j] = (isA ? a.q : a.w) + (size_t)(g < lim ? g : 0) * K + gc * 16;
   }
   auto issue = [&](uint32_t kt) {
     int8_t* base = lds + (kt % S) * STAGE;
 #pragma unroll
     for (int j = 0; j < L; ++j)
-      __builtin_amdgcn_global_load_lds((const void*)(src[j] + (size_t)kt * 64),
+      __builtin_amdgcn_global_load_lds((const void*)(src[j] + (size_t)kt * 128),
                                        W8A8_LDS_PTR(base + (wave * L + j) * 1024 + lane * 16), 16, 0, 0);
   };
-  const int fr = lane & 31, fhalf = lane >> 5;
-  int foff[2];
+  const int fr = lane & 31, fh = lane >> 5;
+  int off[4];
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
-    foff[s] = (fr >> 4) * 1024 + (4 * (fr & 15) + ((2 * s + fhalf) ^ lds_swizzle(fr & 15))) * 16;
-
+  for (int i = 0; i < 4; ++i) off[i] = fr * 128 + (((2 * i + fh) ^ (fr & 7)) * 16);
   v16i acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
-
+  auto rd = [&](uint32_t kt, int i, v4i (&af)[FM], v4i (&bf)[FN]) {
+    const int8_t* base = lds + (kt % S) * STAGE;
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < (int)KT) issue(s);
-  for (uint32_t kt = 0; kt < KT; ++kt) {
-    // Stage kt must have landed: of this wave's outstanding DMA groups only
-    // the ones issued after it (stages kt+1 .. min(KT-1, kt+S-2)) may remain.
-    const uint32_t newer = min(KT - 1, kt + S - 2) - kt;
-    if (newer >= (uint32_t)(S - 2)) wait_vmcnt<(S - 2) * L>();
-    else if (newer == 3) wait_vmcnt<3 * L>();
+    for (int f = 0; f < FM; ++f) af[f] = *(const v4i*)(base + (wm0 + 32 * f) * 128 + off[i]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(base + (BM + wn0 + 32 * j) * 128 + off[i]);
+  };
+  auto mm = [&](const v4i (&af)[FM], const v4i (&bf)[FN]) {
+#pragma unroll
+    for (int f = 0; f < FM; ++f)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[f][j] = mfma32(af[f], bf[j], acc[f][j]);
+  };
+  // This wave's part of stage s has landed once at most (newer stages issued) x L
+  // DMA loads remain outstanding; loads complete in issue order.
+  auto wait_landed = [&](uint32_t newer) {
+    if (newer >= 3) wait_vmcnt<3 * L>();
     else if (newer == 2) wait_vmcnt<2 * L>();
     else if (newer == 1) wait_vmcnt<L>();
     else wait_vmcnt<0>();
-    // all waves' parts of stage kt are in LDS, and every wave has finished
-    // reading stage kt-1, whose buffer the next DMA overwrites
-    __builtin_amdgcn_s_barrier();
-    if (kt + S - 1 < KT) issue(kt + S - 1);
-    const int8_t* base = lds + (kt % S) * STAGE;
+  };
+
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      v4i af[FM], bf[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = *(const v4i*)(base + ((wm0 / 32 + i) * 2) * 1024 + foff[s]);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(base + (AB + (wn0 / 32 + j) * 2) * 1024 + foff[s]);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
-    }
+  for (int s = 0; s < S; ++s)
+    if (s < (int)KT) issue(s);
+  v4i a0[FM], b0[FN], a1[FM], b1[FN];
+  wait_landed(min(KT - 1, (uint32_t)S - 1));
+  __builtin_amdgcn_s_barrier();
+  rd(0, 0, a0, b0);
+  // Fragments of the next sub-step are read while the current one's MFMAs
+  // run.  The loop body has no branch between a read and its use, so the
+  // compiler's LDS waits keep the newest reads in flight.
+  for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+    rd(kt, 1, a1, b1);
+    mm(a0, b0);
+    rd(kt, 2, a0, b0);
+    mm(a1, b1);
+    rd(kt, 3, a1, b1);
+    mm(a0, b0);
+    // stages issued so far: 0 .. min(KT - 1, kt + S - 1); stage kt + 1 must have landed
+    wait_landed(min(KT - 1, kt + S - 1) - (kt + 1));
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of stage kt returned
+    __builtin_amdgcn_s_barrier();         // all waves: stage kt + 1 landed, stage kt read
+    if (kt + S < KT) issue(kt + S);       // into stage kt's slot
+    rd(kt + 1, 0, a0, b0);
+    mm(a1, b1);
   }
+  rd(KT - 1, 1, a1, b1);
+  mm(a0, b0);
+  rd(KT - 1, 2, a0, b0);
+  mm(a1, b1);
+  rd(KT - 1, 3, a1, b1);
+  mm(a0, b0);
+  mm(a1, b1);
+
   // 32x32 result layout: lane l, value v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
@@ -357,7 +387,7 @@ __global__ __launch_bounds__(256) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
 template <int BM, int BN, int WM, int WN, int S>
 static void launch_dma(hipStream_t st, const GemmArgs& a) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
-  const dim3 grid(tm * tn), block(256);
+  const dim3 grid(tm * tn), block(512);
   if (a.out_dtype == W8A8_OUT_I32)
     hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_I32>), grid, block, 0, st, a, tm, tn);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
@@ -380,14 +410,22 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
     hipLaunchKernelGGL((gemm_skinny<2, 4, 4>), dim3(nb16, 1), dim3(256), 0, st, a);
   } else if (a.m <= 64) {
     hipLaunchKernelGGL((gemm_skinny<4, 4, 2>), dim3(nb16, 1), dim3(256), 0, st, a);
-  } else if (a.k % 64 == 0) {
-    // measured on MI355X (Qwen3-8B shapes at M = 129 and 512)
-    if (a.n >= 16384 && a.m >= 256)
-      launch_dma<256, 192, 128, 96, 4>(st, a);
-    else if (a.n >= 16384)
-      launch_dma<128, 192, 64, 96, 5>(st, a);
+  } else if (a.k % 128 == 0) {
+    // Tile per problem, measured on MI355X at M = 129 / 512 on the Qwen3-8B
+    // projection shapes: the largest tile that still gives about one tile
+    // per CU, smaller tiles for narrow N.
+    const uint64_t t256 = (uint64_t)((a.m + 255) / 256) * ((a.n + 191) / 192);
+    const uint64_t t128 = (uint64_t)((a.m + 127) / 128) * ((a.n + 191) / 192);
+    if (t256 >= 240)
+      launch_dma<256, 192, 64, 96, 2>(st, a);
+    else if (t128 >= 240)
+      launch_dma<128, 192, 32, 96, 3>(st, a);
+    else if (a.n >= 6144 && a.m >= 256)
+      launch_dma<128, 128, 32, 64, 4>(st, a);
+    else if (a.m >= 128)
+      launch_dma<128, 64, 32, 32, 4>(st, a);
     else
-      launch_dma<64, 128, 32, 64, 6>(st, a);
+      launch_dma<64, 128, 32, 32, 4>(st, a);
   } else {
     constexpr int BM = 128, BN = 128;
     const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
