@@ -20,6 +20,10 @@ generator (bitemyapp/inferrous, crates/inferrous-qwen3/tools/operator_fixtures.p
   src/conformance.rs:663).  The reference draws its rope/attention inputs
   before this case; those draws are not repeated, so ``up`` differs from the
   reference's own file while following the same recipe.
+* weight_quantize (tools/prepare.py:79-83, offline weight quantization):
+  BF16 weights [33, 4096] (row 0 zero, row 1 with +-127 and .5 ties) as BF16
+  bits, expected ``scale = amax(|w|, 1).clamp(min=1e-8) / 127`` and
+  ``q = round(w / scale).clamp(-127, 127)`` per output channel.
 
 Expected values are computed here with torch on the CPU -- an implementation
 independent of the C oracle in oracle/ -- and stored with the inputs.  The
@@ -101,6 +105,14 @@ def main() -> None:
     up = to_bf16_values(torch.randn(12288))
     act = to_bf16_values(torch.nn.functional.silu(gate) * up)
     out.add("swiglu", {"gate": gate, "up": up, "out": act})
+
+    w = torch.randn(33, 4096).bfloat16()
+    w[0] = 0
+    w[1, :8] = ties.bfloat16()
+    wf = w.float()
+    wscale = wf.abs().amax(1, keepdim=True).clamp(min=1e-8) / 127.0
+    wq = torch.round(wf / wscale).clamp(-127, 127).to(torch.int8)
+    out.add("weight_quantize", {"w": w.view(torch.int16), "q": wq, "scale": wscale.flatten()})
 
     manifest = {"generator": "tests/golden/make_fixtures.py", "torch": torch.__version__,
                 "seed": 824, "cases": out.cases}

@@ -71,6 +71,20 @@ def test_quantize_fixtures(env, fixtures):
         assert np.array_equal(bits(sc2.to_host_vec(s)), bits(fixtures.tensor(c, "scale").reshape(-1)))
 
 
+def test_weight_quantize_fixture(env, fixtures):
+    """tools/prepare.py:79-83 on the device (w8a8_quantize_bf16, one row per
+    output channel)."""
+    ctx, mod, s = env
+    (c,) = fixtures.cases("weight_quantize")
+    w = fixtures.tensor(c, "w").view(np.uint16)
+    n, k = w.shape
+    q = DeviceBuffer.zeroed(s, n * k, np.int8)
+    sc = DeviceBuffer.zeroed(s, n, np.float32)
+    mod.quantize_weights(s, dev(s, w.reshape(-1)), k, q, sc)
+    assert np.array_equal(q.to_host_vec(s), fixtures.tensor(c, "q").reshape(-1))
+    assert np.array_equal(bits(sc.to_host_vec(s)), bits(fixtures.tensor(c, "scale")))
+
+
 @pytest.mark.parametrize("width", [16, 128, 1000, 1001, 4096, 12288, 16400, 20000])
 def test_quantize_widths_edges_and_bf16(env, width):
     ctx, mod, s = env

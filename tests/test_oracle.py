@@ -64,6 +64,16 @@ def test_quantize_matches_fixtures(fixtures):
         assert np.array_equal(bits(s), bits(fixtures.tensor(c, "scale").reshape(-1))), c["name"]
 
 
+def test_weight_quantize_matches_prepare_recipe(fixtures):
+    # tools/prepare.py:79-83: per-output-channel quantization of BF16 weights
+    (c,) = fixtures.cases("weight_quantize")
+    w = fixtures.tensor(c, "w").view(np.uint16)
+    q, s = oracle.quantize_bf16(w, w.shape[1])
+    assert np.array_equal(q, fixtures.tensor(c, "q").reshape(-1))
+    assert np.array_equal(bits(s), bits(fixtures.tensor(c, "scale")))
+    assert q.min() >= -127 and (s > 0).all()
+
+
 def test_quantize_kats():
     # zero row: scale is the floor 1e-8/127, all q zero
     q, s = oracle.quantize(np.zeros(4096, F32), 4096)
