@@ -148,6 +148,21 @@ int w8a8_linear_residual(void *stream, const int8_t *q, const float *asc,
                          uint32_t k, const float *residual, void *out,
                          void *combined, int out_dtype);
 
+/* `quantize_with_max` (src/kernels.rs:453-475) feeding `linear_residual`
+ * (src/kernels.rs:577-618) or `linear`, the decode chain of
+ * GpuModel::linear_residual at K = 12288 (src/gpu.rs:371-406): q / scales
+ * receive the quantized activations exactly as w8a8_quantize_with_max
+ * writes them, and out / combined exactly as w8a8_linear_residual (or
+ * w8a8_linear when residual is NULL) computes them from q / scales.  At
+ * m == 1 with k in {4096, 12288} this is one launch (the quantization runs
+ * inside the GEMV); otherwise the two steps run back to back. */
+int w8a8_linear_quantize_with_max(void *stream, const float *x,
+                                  const uint32_t *maxima, size_t m, uint32_t k,
+                                  int8_t *q, float *scales, const int8_t *w,
+                                  const float *ws, size_t n,
+                                  const float *residual, void *out,
+                                  void *combined, int out_dtype);
+
 /* `linear_pair` (src/kernels.rs:696-735), `linear_triple`
  * (src/kernels.rs:736-806) and the gate/up projections of `linear_swiglu`
  * (src/kernels.rs:619-695): `count` (1..4) sibling projections that share

@@ -377,6 +377,39 @@ int w8a8_linear_residual(void* stream, const int8_t* q, const float* asc, size_t
                     residual, combined);
 }
 
+int w8a8_linear_quantize_with_max(void* stream, const float* x, const uint32_t* maxima, size_t m,
+                                  uint32_t k, int8_t* q, float* scales, const int8_t* w,
+                                  const float* ws, size_t n, const float* residual, void* out,
+                                  void* combined, int out_dtype) {
+  if (residual && out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  int s = check_linear(q, scales, m, w, ws, n, k, out, out_dtype);
+  if (s != W8A8_OK) return s;
+  if (m == 0) return W8A8_OK;
+  if (!x || !maxima || !q || !scales) return W8A8_ENULL;
+  if ((residual == nullptr) != (combined == nullptr)) return W8A8_ENULL;
+  if (!al(x, 16) || !al(maxima, 4) || !al(residual, 4) || !al(combined, out_align(out_dtype)))
+    return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  hipStream_t st = (hipStream_t)stream;
+  if (m == 1 && n > 0 && (k == 4096 || k == 12288)) {
+    GemvArgs a{};
+    a.m = 1;
+    a.k = k;
+    a.count = 1;
+    a.w[0] = w;
+    a.ws[0] = ws;
+    a.n[0] = (uint32_t)n;
+    a.out[0] = out;
+    a.out_dtype = out_dtype;
+    a.residual = residual;
+    a.combined = combined;
+    return hip_status(launch_gemv_quantize_with_max(st, a, x, maxima, q, scales));
+  }
+  s = hip_status(launch_quantize_with_max(st, x, k, m, maxima, q, scales));
+  if (s != W8A8_OK || n == 0) return s;
+  return run_linear(st, q, scales, m, w, ws, n, k, out, out_dtype, W8A8_PATH_AUTO, residual, combined);
+}
+
 int w8a8_linear_grouped(void* stream, const int8_t* q, const float* asc, size_t m, uint32_t k,
                         int count, const int8_t* const* w, const float* const* ws, const size_t* n,
                         void* const* out, int out_dtype) {

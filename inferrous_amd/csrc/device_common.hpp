@@ -44,6 +44,14 @@ __device__ __forceinline__ float dequant(int32_t acc, float asc, float ws) {
   return bf16_rne(t * ws);
 }
 
+// Four quantized codes round(RN(v / s)) packed little-endian into one word
+// (src/kernels.rs:449-451: RN division, then the clamp / ties-even round).
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float s) {
+  uint32_t q0 = (uint8_t)round_i8(a / s), q1 = (uint8_t)round_i8(b / s);
+  uint32_t q2 = (uint8_t)round_i8(c / s), q3 = (uint8_t)round_i8(d / s);
+  return q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
+}
+
 // SiLU(g) * u in the reference's operation order (src/kernels.rs:681,
 // :2181): bf(RN(RN(g / RN(1 + exp(-g))) * u)).  exp is the ROCm device
 // library's expf (accurate to about 1 ulp); the reference uses an

@@ -28,12 +28,6 @@ __device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
   return max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
-__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float s) {
-  uint32_t q0 = (uint8_t)round_i8(a / s), q1 = (uint8_t)round_i8(b / s);
-  uint32_t q2 = (uint8_t)round_i8(c / s), q3 = (uint8_t)round_i8(d / s);
-  return q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
-}
-
 // f32 rows, width % 4 == 0, 16-byte aligned rows.
 __global__ __launch_bounds__(kQThreads) void quantize_f32_vec(
     const float* __restrict__ x, uint32_t width, int8_t* __restrict__ q,

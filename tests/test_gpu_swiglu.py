@@ -215,3 +215,114 @@ def test_decode_mlp_chain_and_graph_replay(env):
                         ("hidden", hidden)):
             assert np.array_equal(b.to_host_vec(s).view(np.uint8), eager[name].view(np.uint8)), \
                 f"replay {rep}: {name}"
+
+
+@pytest.mark.parametrize("m,k,n,res,dtype", [(1, 12288, 4096, True, np.float32),
+                                             (1, 12288, 4099, True, np.uint16),
+                                             (1, 4096, 12288, False, np.float32),
+                                             (1, 4096, 33, False, np.int32),
+                                             (3, 12288, 100, True, np.float32),
+                                             (1, 1024, 64, False, np.float32)])
+def test_linear_quantize_with_max_matches_two_steps(env, m, k, n, res, dtype):
+    """The fused quantize_with_max + linear(_residual) equals the two launches
+    (src/gpu.rs:371-406) and the oracle, bit for bit."""
+    ctx, mod, s = env
+    print(f"linear_quantize_with_max m={m} k={k} n={n} res={res} {np.dtype(dtype).name}", flush=True)
+    rng = np.random.default_rng(k + n + m)
+    x = oracle.bf16_rne((rng.standard_normal(m * k) * 3).astype(F32))
+    x[5] = 0.0
+    mx = np.array([oracle.absmax_bits(r) for r in x.reshape(m, k)], np.uint32)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = (rng.random(n) / 512 + 1e-5).astype(F32)
+    resid = oracle.bf16_rne(rng.standard_normal(m * n).astype(F32))
+    dx, dmx, dw, dws, dres = dev(s, x), dev(s, mx), dev(s, w), dev(s, ws), dev(s, resid)
+
+    def outputs():
+        q = DeviceBuffer.zeroed(s, m * k, np.int8)
+        sc = DeviceBuffer.zeroed(s, m, np.float32)
+        out = DeviceBuffer.zeroed(s, m * n, dtype)
+        comb = DeviceBuffer.zeroed(s, m * n, dtype) if res else None
+        return q, sc, out, comb
+
+    q1, sc1, out1, comb1 = outputs()
+    mod.linear_quantize_with_max(s, None, dx, k, dmx, q1, sc1, dw, dws, out1,
+                                 dres if res else None, comb1)
+    q2, sc2, out2, comb2 = outputs()
+    mod.quantize_with_max(s, None, dx, k, dmx, q2, sc2)
+    if res:
+        mod.linear_residual(s, None, q2, sc2, dw, dws, k, dres, out2, comb2)
+    else:
+        mod.linear(s, None, q2, sc2, dw, dws, k, out2)
+    for a, b in ((q1, q2), (sc1, sc2), (out1, out2)) + (((comb1, comb2),) if res else ()):
+        assert np.array_equal(a.to_host_vec(s).view(np.uint8), b.to_host_vec(s).view(np.uint8))
+    oq, osc = oracle.quantize_with_max(x, k, mx)
+    assert np.array_equal(q1.to_host_vec(s), oq)
+    acc, of, ob = oracle.linear(oq, osc, w, ws, k, threads=8)
+    got = out1.to_host_vec(s)
+    if dtype == np.int32:
+        assert np.array_equal(got, acc)
+    elif dtype == np.uint16:
+        assert np.array_equal(got, ob)
+    else:
+        assert np.array_equal(bits(got), bits(of))
+    if res:
+        want = oracle.residual(resid, of)
+        gotc = comb1.to_host_vec(s)
+        if dtype == np.uint16:
+            assert np.array_equal(gotc, (bits(want) >> 16).astype(np.uint16))
+        else:
+            assert np.array_equal(bits(gotc), bits(want))
+
+
+def test_decode_mlp_chain_fused_down_quantize(env):
+    """The decode MLP block with the down quantization fused into the down
+    GEMV equals the unfused chain bit for bit, eagerly and under graph replay."""
+    ctx, mod, s = env
+    rng = np.random.default_rng(77)
+    h, f = 4096, 12288
+    x = oracle.bf16_rne(rng.standard_normal(h).astype(F32))
+    res = oracle.bf16_rne(rng.standard_normal(h).astype(F32))
+    wg = dev(s, rng.integers(-127, 128, (f, h), dtype=np.int8))
+    wu = dev(s, rng.integers(-127, 128, (f, h), dtype=np.int8))
+    wd = dev(s, rng.integers(-127, 128, (h, f), dtype=np.int8))
+    sg = dev(s, (rng.random(f) / 4096 + 1e-5).astype(F32))
+    su = dev(s, (rng.random(f) / 4096 + 1e-5).astype(F32))
+    sd = dev(s, (rng.random(h) / 4096 + 1e-5).astype(F32))
+    dx, dres = dev(s, x), dev(s, res)
+
+    def buffers():
+        return dict(q4=DeviceBuffer.zeroed(s, h, np.int8), sc4=DeviceBuffer.zeroed(s, 1, np.float32),
+                    mx=DeviceBuffer.zeroed(s, 1, np.uint32),
+                    g=DeviceBuffer.zeroed(s, f, np.float32), u=DeviceBuffer.zeroed(s, f, np.float32),
+                    act=DeviceBuffer.zeroed(s, f, np.float32),
+                    q12=DeviceBuffer.zeroed(s, f, np.int8), sc12=DeviceBuffer.zeroed(s, 1, np.float32),
+                    down=DeviceBuffer.zeroed(s, h, np.float32), hid=DeviceBuffer.zeroed(s, h, np.float32))
+
+    def block(b, fused):
+        mod.quantize(s, None, dx, h, b["q4"], b["sc4"], maxima_reset=b["mx"])
+        mod.linear_swiglu(s, None, b["q4"], b["sc4"], h, wg, sg, b["g"], wu, su, b["u"], b["act"], b["mx"])
+        if fused:
+            mod.linear_quantize_with_max(s, None, b["act"], f, b["mx"], b["q12"], b["sc12"], wd, sd,
+                                         b["down"], dres, b["hid"])
+        else:
+            mod.quantize_with_max(s, None, b["act"], f, b["mx"], b["q12"], b["sc12"])
+            mod.linear_residual(s, None, b["q12"], b["sc12"], wd, sd, f, dres, b["down"], b["hid"])
+
+    ref, fus = buffers(), buffers()
+    block(ref, False)
+    block(fus, True)
+    names = ("q12", "sc12", "down", "hid", "mx")
+    want = {k: ref[k].to_host_vec(s).view(np.uint8).copy() for k in names}
+    for k in names:
+        assert np.array_equal(fus[k].to_host_vec(s).view(np.uint8), want[k]), k
+    graph = Graph(s)
+    with graph:
+        block(fus, True)
+    for rep in range(3):
+        for k in ("q12", "down", "hid"):
+            fus[k].fill_zero(s)
+        s.synchronize()
+        graph.launch()
+        s.synchronize()
+        for k in names:
+            assert np.array_equal(fus[k].to_host_vec(s).view(np.uint8), want[k]), f"replay {rep}: {k}"
