@@ -280,6 +280,50 @@ def main() -> int:
         ms = time_graph(capture(lambda: decode_step(with_quant=True)), 20)
         extras["decode_step_with_quantize"] = {"ms": round(ms, 4),
                                                "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1)}
+        # The reference's decode layer chain (src/gpu.rs:571-790) with this
+        # library's ops: quantize (maxima reset) -> qkv; quantize -> o with
+        # residual; quantize (reset) -> linear_swiglu (publishes max |act|)
+        # -> quantize_with_max + down with residual.  gate and up
+        # are the two halves of the gate_up matrix.  Weight bytes as the
+        # headline (the small activation/output traffic is not counted).
+        ffn = 12288
+        resid = DeviceBuffer.from_host(s, synth.normal_rows(43, 1, 4096).reshape(-1))
+        mx = DeviceBuffer.zeroed(s, 1, np.uint32)
+        gbuf = DeviceBuffer.zeroed(s, ffn, np.float32)
+        ubuf = DeviceBuffer.zeroed(s, ffn, np.float32)
+        act = DeviceBuffer.zeroed(s, ffn, np.float32)
+        comb = DeviceBuffer.zeroed(s, 4096, np.uint16)
+        q4, sc4 = qs[4096]
+        q12, sc12 = qs[12288]
+        halves = []
+        for mats in layers:
+            (_, _, _, gw, gws) = mats[2]
+            halves.append((DeviceBuffer.view_of(gw, 0, ffn * 4096), DeviceBuffer.view_of(gws, 0, ffn),
+                           DeviceBuffer.view_of(gw, ffn * 4096, ffn * 4096),
+                           DeviceBuffer.view_of(gws, ffn, ffn)))
+
+        def layer_chain():
+            for mats, (wg_, sg_, wu_, su_) in zip(layers, halves):
+                (_, _, _, wqkv, sqkv), (_, _, _, wo, so), _, (_, _, _, wd, sd) = mats
+                mod.quantize(s, None, xs[4096], 4096, q4, sc4, maxima_reset=mx)
+                mod.linear(s, None, q4, sc4, wqkv, sqkv, 4096, outs["qkv"])
+                mod.quantize(s, None, xs[4096], 4096, q4, sc4)
+                mod.linear_residual(s, None, q4, sc4, wo, so, 4096, resid, outs["o"], comb)
+                mod.quantize(s, None, xs[4096], 4096, q4, sc4, maxima_reset=mx)
+                mod.linear_swiglu(s, None, q4, sc4, 4096, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx)
+                mod.linear_quantize_with_max(s, None, act, ffn, mx, q12, sc12, wd, sd, outs["down"],
+                                             resid, comb)
+            mod.quantize(s, None, xs[hk], hk, q4, sc4)
+            mod.linear_argmax(s, q4, sc4, head_w, head_s, hk, token)
+
+        layer_chain()
+        s.synchronize()
+        ms = time_graph(capture(layer_chain), 20)
+        extras["decode_reference_chain"] = {
+            "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "launches": 8 * synth.LAYERS + 3,
+            "chain": "quantize, qkv, quantize, o+residual, quantize, linear_swiglu, quantize_with_max, down+residual; lm_head"}
+        log(f"reference decode chain: {ms * 1e3:.1f} us ({extras['decode_reference_chain']['GB/s']} GB/s)")
         # prefill (config 4): M = 512 TOPS and M = 129 HBM GB/s, 36 layers x 4 shapes
         pre = {}
         for m in (512, 129):

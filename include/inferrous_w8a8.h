@@ -153,9 +153,8 @@ int w8a8_linear_residual(void *stream, const int8_t *q, const float *asc,
  * GpuModel::linear_residual at K = 12288 (src/gpu.rs:371-406): q / scales
  * receive the quantized activations exactly as w8a8_quantize_with_max
  * writes them, and out / combined exactly as w8a8_linear_residual (or
- * w8a8_linear when residual is NULL) computes them from q / scales.  At
- * m == 1 with k in {4096, 12288} this is one launch (the quantization runs
- * inside the GEMV); otherwise the two steps run back to back. */
+ * w8a8_linear when residual is NULL) computes them from q / scales.  The two
+ * steps run back to back on the stream. */
 int w8a8_linear_quantize_with_max(void *stream, const float *x,
                                   const uint32_t *maxima, size_t m, uint32_t k,
                                   int8_t *q, float *scales, const int8_t *w,

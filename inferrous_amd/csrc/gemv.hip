@@ -302,65 +302,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_swiglu(SwigluArgs a) {
   if (a.maxima) publish_absmax_block(bits, a.maxima);
 }
 
-// quantize_with_max (src/kernels.rs:453-475) fused into the M = 1 GEMV.  The
-// waves first issue their weight loads (R rows each), then the workgroup
-// quantizes the f32 activation row once into LDS with the producer-published
-// maximum -- s = RN(m / 127), q = round(RN(x / s)), the same arithmetic as
-// the stand-alone kernel -- and the dot products read their activation
-// chunks from LDS.  The HBM stream of the weights overlaps the quantization;
-// x is read from L2 once per workgroup, as often as the int8 row would be.
-template <int R, int KC, int EPI>
-__global__ __launch_bounds__(kGemvThreads) void gemv_qwm(GemvArgs a, const float* __restrict__ x,
-                                                          const uint32_t* __restrict__ maxima,
-                                                          int8_t* __restrict__ q_out,
-                                                          float* __restrict__ scale_out) {
-  __shared__ __attribute__((aligned(16))) int8_t qs[KC * 1024];
-  const int lane = threadIdx.x & 63;
-  const uint32_t g = blockIdx.x * kGemvWaves + wave_id();
-  const uint32_t n = a.n[0];
-  const uint32_t row0 = g * R;
-  const bool live = row0 < n;
-  constexpr uint32_t K = KC * 1024;
-  v4i wv[R][KC];
-  if (live) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int8_t* p = a.w[0] + (size_t)min(row0 + r, n - 1) * K + lane * 16;
-#pragma unroll
-      for (int c = 0; c < KC; ++c) wv[r][c] = load_nt16(p + c * 1024);
-    }
-  }
-  const float s = __uint_as_float(maxima[0]) / 127.0f;
-#pragma unroll
-  for (int i = 0; i < KC; ++i) {  // K / 4 float4 over 256 threads
-    const int v = i * kGemvThreads + threadIdx.x;
-    const v4f xv = reinterpret_cast<const v4f*>(x)[v];
-    const uint32_t packed = pack4(xv.x, xv.y, xv.z, xv.w, s);
-    reinterpret_cast<uint32_t*>(qs)[v] = packed;
-    if (blockIdx.x == 0) reinterpret_cast<uint32_t*>(q_out)[v] = packed;  // the q / scales outputs
-  }
-  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
-  __syncthreads();
-  int acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0;
-  if (live) {
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const v4i xq = *reinterpret_cast<const v4i*>(qs + c * 1024 + lane * 16);
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = dot16(xq, wv[r][c], acc[r]);
-    }
-  }
-  const int total = reduce_to_lanes<R>(acc, lane);
-  const uint32_t row = row0 + lane;
-  if (live && lane < R && row < n) {
-    const float value = dequant(total, s, a.ws[0][row]);
-    if (a.out[0]) store_out(a.out[0], row, a.out_dtype, total, value);
-    if (EPI == EPI_RESIDUAL) store_out(a.combined, row, a.out_dtype, total, bf16_rne(a.residual[row] + value));
-  }
-}
-
 __device__ __forceinline__ float load_val(const void* p, size_t i, int dtype) {
   if (dtype == W8A8_OUT_BF16)
     return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
@@ -478,28 +419,6 @@ hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
-}
-
-template <int R, int KC>
-static hipError_t launch_qwm(hipStream_t st, GemvArgs& a, const float* x, const uint32_t* maxima,
-                             int8_t* q, float* scales) {
-  const uint32_t groups = (a.n[0] + R - 1) / R;
-  const dim3 grid((groups + kGemvWaves - 1) / kGemvWaves);
-  if (a.residual)
-    hipLaunchKernelGGL((gemv_qwm<R, KC, EPI_RESIDUAL>), grid, dim3(kGemvThreads), 0, st, a, x, maxima,
-                       q, scales);
-  else
-    hipLaunchKernelGGL((gemv_qwm<R, KC, EPI_PLAIN>), grid, dim3(kGemvThreads), 0, st, a, x, maxima, q,
-                       scales);
-  return hipGetLastError();
-}
-
-hipError_t launch_gemv_quantize_with_max(hipStream_t st, GemvArgs& a, const float* x,
-                                         const uint32_t* maxima, int8_t* q, float* scales) {
-  if (a.n[0] == 0) return hipSuccess;
-  if (a.k == 4096) return launch_qwm<2, 4>(st, a, x, maxima, q, scales);
-  if (a.k == 12288) return launch_qwm<2, 12>(st, a, x, maxima, q, scales);
-  return hipErrorInvalidValue;
 }
 
 hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_t rows,

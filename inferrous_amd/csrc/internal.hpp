@@ -69,11 +69,6 @@ hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a);  // m == 1, k in {4096, 12288}
-// quantize_with_max fused into the m == 1 GEMV (count == 1, k in {4096, 12288});
-// a.q / a.asc unused: the activation comes from x (f32) and maxima[0]; the
-// codes and the scale are also written to q / scales.
-hipError_t launch_gemv_quantize_with_max(hipStream_t st, GemvArgs& a, const float* x,
-                                         const uint32_t* maxima, int8_t* q, float* scales);
 hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_t rows,
                          uint32_t width, void* act, int dtype, uint32_t* maxima);
 hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* slots, uint32_t* token);

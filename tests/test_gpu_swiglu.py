@@ -224,8 +224,8 @@ def test_decode_mlp_chain_and_graph_replay(env):
                                              (3, 12288, 100, True, np.float32),
                                              (1, 1024, 64, False, np.float32)])
 def test_linear_quantize_with_max_matches_two_steps(env, m, k, n, res, dtype):
-    """The fused quantize_with_max + linear(_residual) equals the two launches
-    (src/gpu.rs:371-406) and the oracle, bit for bit."""
+    """The combined quantize_with_max + linear(_residual) entry point equals
+    the two separate calls (src/gpu.rs:371-406) and the oracle, bit for bit."""
     ctx, mod, s = env
     print(f"linear_quantize_with_max m={m} k={k} n={n} res={res} {np.dtype(dtype).name}", flush=True)
     rng = np.random.default_rng(k + n + m)
@@ -274,9 +274,10 @@ def test_linear_quantize_with_max_matches_two_steps(env, m, k, n, res, dtype):
             assert np.array_equal(bits(gotc), bits(want))
 
 
-def test_decode_mlp_chain_fused_down_quantize(env):
-    """The decode MLP block with the down quantization fused into the down
-    GEMV equals the unfused chain bit for bit, eagerly and under graph replay."""
+def test_decode_mlp_chain_combined_down_entry(env):
+    """The decode MLP block through the combined down entry point
+    (linear_quantize_with_max) equals the chain of separate calls bit for
+    bit, eagerly and under graph replay."""
     ctx, mod, s = env
     rng = np.random.default_rng(77)
     h, f = 4096, 12288
