@@ -95,6 +95,40 @@ def traffic_run() -> int:
     return 0
 
 
+def prefill_profile_run() -> int:
+    """Workload for a kernel-trace profile of the prefill GEMMs: 8 layers of
+    distinct weights (1.5 GB, above the MALL), the four projections at
+    M = 512 and M = 129, three eager passes each (no graphs)."""
+    from inferrous_amd import CudaContext, DeviceBuffer, load, synth
+    ctx = CudaContext(0)
+    mod = load(ctx)
+    s = ctx.new_stream()
+    nl = 8
+    mats = []
+    for layer in range(nl):
+        for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
+            w = DeviceBuffer.zeroed(s, n * k, np.int8)
+            ws = DeviceBuffer.zeroed(s, n, np.float32)
+            mod.synth_i8(s, w, SEED_W, synth.weight_stream(layer, si))
+            mod.synth_f32(s, ws, SEED_S, synth.scale_stream(layer, si), 1e-3, 1e-2)
+            mats.append((name, n, k, w, ws))
+    for m in (512, 129):
+        pq = {}
+        for k, seed in ((4096, 700), (12288, 703)):
+            x = synth.student_t_rows(seed, m, k).reshape(-1)
+            q = DeviceBuffer.zeroed(s, m * k, np.int8)
+            sc = DeviceBuffer.zeroed(s, m, np.float32)
+            mod.quantize(s, None, DeviceBuffer.from_host(s, x), k, q, sc)
+            pq[k] = (q, sc)
+        outs = {name: DeviceBuffer.zeroed(s, m * n, np.uint16) for (name, n, _) in synth.DECODE_SHAPES}
+        for _ in range(3):
+            for (name, n, k, w, ws) in mats:
+                mod.linear(s, None, pq[k][0], pq[k][1], w, ws, k, outs[name])
+        s.synchronize()
+        print(f"prefill M={m} done", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +138,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the counter-profiling workload (gate_up GEMVs + calibration copy)")
+    ap.add_argument("--prefill-profile", action="store_true",
+                    help="run only the prefill GEMM workload for a kernel-trace profile")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode "
@@ -113,6 +149,8 @@ def main() -> int:
 
     if args.traffic:
         return traffic_run()
+    if args.prefill_profile:
+        return prefill_profile_run()
 
     from inferrous_amd import CudaContext, DeviceBuffer, Event, Graph, load, synth
 
