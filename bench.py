@@ -379,6 +379,8 @@ def main() -> int:
                     for (name, n, k, w, ws) in mats:
                         mod.linear(s, None, pq[k][0], pq[k][1], w, ws, k, pouts[name])
 
+            prefill_chain()       # eager pass: sizes the module's split-K workspace
+            s.synchronize()
             ms = time_graph(capture(prefill_chain), 5, warm=1)
             ops = sum(2 * m * n * k for (_, n, k, _, _) in layers[0]) * synth.LAYERS
             byts = sum(gemv_bytes(n, k, m) for (_, n, k, _, _) in layers[0]) * synth.LAYERS

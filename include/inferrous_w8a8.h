@@ -140,6 +140,23 @@ int w8a8_linear_path(void *stream, const int8_t *q, const float *asc, size_t m,
                      const int8_t *w, const float *ws, size_t n, uint32_t k,
                      void *out, int out_dtype, int path);
 
+/* w8a8_linear / w8a8_linear_path / w8a8_linear_residual in one entry point
+ * with an optional caller-owned workspace (no counterpart in the reference,
+ * whose M > 1 kernels take precomputed tensor maps instead, src/gpu.rs:465-475).
+ * residual == NULL selects plain linear (combined must then be NULL too).
+ * With a workspace of at least w8a8_linear_workspace_bytes(m, n, k) bytes
+ * (16-byte aligned), shapes that gain from it are computed split-K: i32
+ * partial sums in the workspace, added exactly by an epilogue kernel.
+ * Results are identical with or without the workspace; a smaller or NULL
+ * workspace selects the unsplit kernels.  Calls sharing one workspace must
+ * not overlap. */
+size_t w8a8_linear_workspace_bytes(size_t m, size_t n, uint32_t k);
+int w8a8_linear_ex(void *stream, const int8_t *q, const float *asc, size_t m,
+                   const int8_t *w, const float *ws, size_t n, uint32_t k,
+                   const float *residual, void *out, void *combined,
+                   int out_dtype, int path, void *workspace,
+                   size_t workspace_bytes);
+
 /* `linear_residual` (src/kernels.rs:577-618): the linear output plus
  * combined = bf16(RN(residual + out)) (src/kernels.rs:615).  out and
  * combined share out_dtype (F32 or BF16); residual is f32 [m, n]. */

@@ -58,7 +58,8 @@ constexpr size_t kDot4MaxM = 2;
 
 int run_linear(hipStream_t st, const int8_t* q, const float* asc, size_t m, const int8_t* w,
                const float* ws, size_t n, uint32_t k, void* out, int out_dtype, int path,
-               const float* residual, void* combined) {
+               const float* residual, void* combined, void* workspace = nullptr,
+               size_t workspace_bytes = 0) {
   if (m == 0 || n == 0) return W8A8_OK;
   if (path == W8A8_PATH_AUTO) path = m <= kDot4MaxM ? W8A8_PATH_DOT4 : W8A8_PATH_MFMA;
   if (path == W8A8_PATH_DOT4) {
@@ -89,6 +90,8 @@ int run_linear(hipStream_t st, const int8_t* q, const float* asc, size_t m, cons
   g.out_dtype = out_dtype;
   g.residual = residual;
   g.combined = combined;
+  g.partials = static_cast<int32_t*>(workspace);
+  g.partial_bytes = workspace ? workspace_bytes : 0;
   return hip_status(launch_gemm(st, g));
 }
 
@@ -375,6 +378,26 @@ int w8a8_linear_residual(void* stream, const int8_t* q, const float* asc, size_t
   if (!ready()) return W8A8_EINIT;
   return run_linear((hipStream_t)stream, q, asc, m, w, ws, n, k, out, out_dtype, W8A8_PATH_AUTO,
                     residual, combined);
+}
+
+size_t w8a8_linear_workspace_bytes(size_t m, size_t n, uint32_t k) {
+  if (m <= kDot4MaxM || m > kU32Max || n > kU32Max) return 0;
+  return gemm_workspace_bytes((uint32_t)m, (uint32_t)n, k);
+}
+
+int w8a8_linear_ex(void* stream, const int8_t* q, const float* asc, size_t m, const int8_t* w,
+                   const float* ws, size_t n, uint32_t k, const float* residual, void* out,
+                   void* combined, int out_dtype, int path, void* workspace, size_t workspace_bytes) {
+  if (path != W8A8_PATH_AUTO && path != W8A8_PATH_DOT4 && path != W8A8_PATH_MFMA) return W8A8_EARG;
+  if (residual && out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  int s = check_linear(q, asc, m, w, ws, n, k, out, out_dtype);
+  if (s != W8A8_OK || m == 0 || n == 0) return s;
+  if ((residual == nullptr) != (combined == nullptr)) return W8A8_ENULL;
+  if (!al(residual, 4) || !al(combined, out_align(out_dtype)) || !al(workspace, 16))
+    return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return run_linear((hipStream_t)stream, q, asc, m, w, ws, n, k, out, out_dtype, path, residual,
+                    combined, workspace, workspace_bytes);
 }
 
 int w8a8_linear_quantize_with_max(void* stream, const float* x, const uint32_t* maxima, size_t m,

@@ -34,6 +34,8 @@
 //    stage k feeds the MFMAs.  Workgroups are numbered so that the M tiles
 //    sharing one weight panel run on the same XCD (workgroup id mod 8 picks
 //    the XCD), so the panel is fetched into that XCD's L2 once.
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -266,7 +268,8 @@ __device__ __forceinline__ void store_ep(const GemmArgs& a, uint32_t r, uint32_t
 // S stages form a ring; stage kt + S is loaded into stage kt's slot once
 // every wave has finished reading it (one barrier per stage).
 template <int BM, int BN, int WM, int WN, int S, int EP>
-__global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, uint32_t tiles_n) {
+__global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, uint32_t tiles_n,
+                                                uint32_t splits) {
   constexpr int WAVES_N = BN / WN;
   static_assert((BM / WM) * (BN / WN) == 8, "eight waves per workgroup");
   static_assert(WM % 32 == 0 && WN % 32 == 0 && S >= 2 && S <= 4, "tile shape");
@@ -277,14 +280,21 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   constexpr int L = NR / 64;     // DMA loads per wave per stage
   __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
 
-  const uint32_t T = tiles_m * tiles_n;
+  // Split-K (splits > 1, EP_I32 only): workgroup (tile, split) sums K range
+  // [split * K / splits, (split + 1) * K / splits) into i32 slab `split` of
+  // a.out; a separate epilogue kernel adds the slabs (exact) and dequantizes.
+  const uint32_t T = tiles_m * tiles_n, G = T * splits;
   uint32_t Lt = blockIdx.x;
-  if (T % 8 == 0) Lt = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8;
+  if (G % 8 == 0) Lt = (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8;
+  const uint32_t split = Lt / T;
+  Lt %= T;
   const uint32_t m0 = (Lt % tiles_m) * BM, n0 = (Lt / tiles_m) * BN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
-  const uint32_t K = a.k, KT = K / 128;
+  const uint32_t K = a.k, KT = K / 128 / splits;
+  const size_t kbase = (size_t)split * KT * 128;
+  if (EP == EP_I32) a.out = reinterpret_cast<int32_t*>(a.out) + (size_t)split * a.m * a.n;
 
   // Sources of this wave's DMA blocks; rows past M / N re-read row 0 (their
   // products only reach accumulator cells that are never stored).
@@ -296,7 +306,7 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
     const bool isA = row < BM;
     const uint32_t g = isA ? m0 + row : n0 + (row - BM);
     const uint32_t lim = isA ? a.m : a.n;
-    src[j] = (isA ? a.q : a.w) + (size_t)(g < lim ? g : 0) * K + gc * 16;
+    src[j] = (isA ? a.q : a.w) + (size_t)(g < lim ? g : 0) * K + kbase + gc * 16;
   }
   auto issue = [&](uint32_t kt) {
     int8_t* base = lds + (kt % S) * STAGE;
@@ -389,15 +399,83 @@ static void launch_dma(hipStream_t st, const GemmArgs& a) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
   const dim3 grid(tm * tn), block(512);
   if (a.out_dtype == W8A8_OUT_I32)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_I32>), grid, block, 0, st, a, tm, tn);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_I32>), grid, block, 0, st, a, tm, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32_RES>), grid, block, 0, st, a, tm, tn);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32_RES>), grid, block, 0, st, a, tm, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32>), grid, block, 0, st, a, tm, tn);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32>), grid, block, 0, st, a, tm, tn, 1u);
   else if (a.residual)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16_RES>), grid, block, 0, st, a, tm, tn);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16_RES>), grid, block, 0, st, a, tm, tn, 1u);
   else
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16>), grid, block, 0, st, a, tm, tn);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16>), grid, block, 0, st, a, tm, tn, 1u);
+}
+
+// Split-K epilogue: out[r][c] = epilogue(sum over slabs of partials[s][r][c]).
+// The i32 sum is exact in any order.  Four columns per thread.
+template <int EP>
+__global__ __launch_bounds__(256) void splitk_epilogue(GemmArgs a, const int32_t* __restrict__ partials,
+                                                        uint32_t splits) {
+  const size_t mn = (size_t)a.m * a.n;
+  for (size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4; i < mn; i += (size_t)gridDim.x * 1024) {
+    v4i acc = *reinterpret_cast<const v4i*>(partials + i);
+    for (uint32_t s = 1; s < splits; ++s) acc += *reinterpret_cast<const v4i*>(partials + s * mn + i);
+    const uint32_t r = (uint32_t)(i / a.n), c = (uint32_t)(i % a.n);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float wsc = EP != EP_I32 ? a.ws[c + j] : 0.f;
+      store_ep<EP>(a, r, c + j, acc[j], wsc);
+    }
+  }
+}
+
+// Split-K plan, measured on MI355X: the K = 12288 down projection (few,
+// long tiles) and the M <= 255 shapes with at most 128 tiles of 128 x 64.
+// tile 0 = 128 x 128, 1 = 128 x 64.
+static bool split_plan(uint32_t m, uint32_t n, uint32_t k, int& tile, uint32_t& splits) {
+  if (m <= 64 || k % 128 != 0 || n % 4 != 0) return false;
+  const uint32_t kt = k / 128;
+  if (k >= 8192) {
+    tile = 0;
+    splits = m >= 256 ? 2 : 4;
+  } else if (m < 256 && (uint64_t)((m + 127) / 128) * ((n + 63) / 64) <= 128) {
+    tile = 1;
+    splits = 2;
+  } else {
+    return false;
+  }
+  return kt % splits == 0 && kt / splits >= 4;
+}
+
+size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
+  int tile;
+  uint32_t splits;
+  if (!split_plan(m, n, k, tile, splits)) return 0;
+  return (size_t)splits * m * n * sizeof(int32_t);
+}
+
+template <int BM, int BN, int WM, int WN, int S>
+static hipError_t launch_split(hipStream_t st, const GemmArgs& a, uint32_t splits) {
+  const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
+  GemmArgs p = a;
+  p.out = a.partials;
+  p.out_dtype = W8A8_OUT_I32;
+  hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_I32>), dim3(tm * tn * splits), dim3(512), 0, st, p,
+                     tm, tn, splits);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t mn = (size_t)a.m * a.n;
+  const unsigned blocks = (unsigned)std::min<size_t>((mn / 4 + 255) / 256, 4096);
+  if (a.out_dtype == W8A8_OUT_I32)
+    hipLaunchKernelGGL(splitk_epilogue<EP_I32>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+  else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
+    hipLaunchKernelGGL(splitk_epilogue<EP_F32_RES>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+  else if (a.out_dtype == W8A8_OUT_F32)
+    hipLaunchKernelGGL(splitk_epilogue<EP_F32>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+  else if (a.residual)
+    hipLaunchKernelGGL(splitk_epilogue<EP_BF16_RES>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+  else
+    hipLaunchKernelGGL(splitk_epilogue<EP_BF16>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -417,6 +495,12 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   } else if (a.m <= 64 && !wide) {
     hipLaunchKernelGGL((gemm_skinny<4, 4, 2>), dim3(nb16, 1), dim3(256), 0, st, a);
   } else if (a.k % 128 == 0) {
+    int tile;
+    uint32_t splits;
+    if (a.partials && split_plan(a.m, a.n, a.k, tile, splits) &&
+        a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))
+      return tile == 0 ? launch_split<128, 128, 32, 64, 4>(st, a, splits)
+                       : launch_split<128, 64, 32, 32, 4>(st, a, splits);
     // Tile per problem, measured on MI355X at M = 129 / 512 on the Qwen3-8B
     // projection shapes: the largest tile that still gives about one tile
     // per CU, smaller tiles for narrow N.

@@ -58,7 +58,12 @@ struct GemmArgs {
   int out_dtype;
   const float* residual;
   void* combined;
+  int32_t* partials;     // optional split-K workspace (i32 slabs), may be null
+  size_t partial_bytes;
 };
+
+// Bytes of split-K workspace launch_gemm would use for this shape (0: none).
+size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 
 hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t width, size_t rows,
                            int8_t* q, float* scales, uint32_t* maxima_reset);

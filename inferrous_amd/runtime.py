@@ -204,6 +204,14 @@ class Event:
             self._p = 0
 
 
+_CAPTURING: set = set()
+
+
+def is_capturing(stream) -> bool:
+    """True while a Graph context is capturing this stream (no allocation then)."""
+    return stream is not None and stream.handle in _CAPTURING
+
+
 class Graph:
     """Capture of everything queued on a (non-default) stream, then replay."""
 
@@ -213,9 +221,11 @@ class Graph:
 
     def __enter__(self):
         check(lib().w8a8_graph_capture_begin(self.stream.handle), "capture begin")
+        _CAPTURING.add(self.stream.handle)
         return self
 
     def __exit__(self, exc_type, exc, tb):
+        _CAPTURING.discard(self.stream.handle)
         p = ctypes.c_void_p()
         st = lib().w8a8_graph_capture_end(self.stream.handle, ctypes.byref(p))
         if exc_type is None:

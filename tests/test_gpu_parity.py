@@ -366,3 +366,75 @@ def test_errors_raise_not_fall_back(env):
     asc = DeviceBuffer.zeroed(s, 1, np.float32)
     with pytest.raises(W8A8Error):
         mod.linear(s, None, q, asc, q, asc, 4095, DeviceBuffer.zeroed(s, 1, np.float32))
+
+
+# ------------------------------------------------------------------ split-K workspace
+@pytest.mark.parametrize("m,n,k", [(129, 4096, 12288), (512, 4096, 12288), (129, 4096, 4096),
+                                   (100, 96, 12288), (255, 1024, 4096)])
+@pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
+def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
+    """w8a8_linear_ex with a workspace (split-K partials + exact i32 epilogue)
+    equals the call without one and the oracle, bit for bit."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    print(f"split-K m={m} n={n} k={k} {np.dtype(dtype).name} res={res}", flush=True)
+    lib = _lib.lib()
+    need = lib.w8a8_linear_workspace_bytes(m, n, k)
+    assert need > 0 and need % (4 * m * n) == 0
+    rng = np.random.default_rng(m * 31 + n + k)
+    q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    q[0] = 127
+    w[0] = 127
+    asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    resid = oracle.bf16_rne(rng.standard_normal(m * n).astype(F32))
+    dq, da, dw, dws, dres = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws), dev(s, resid)
+    work = DeviceBuffer.zeroed(s, need, np.uint8)
+    dt = {np.float32: _lib.OUT_F32, np.uint16: _lib.OUT_BF16, np.int32: _lib.OUT_I32}[dtype]
+    outs = []
+    for wp, wb in ((work.ptr, need), (None, 0), (work.ptr, need - 1)):
+        out = DeviceBuffer.zeroed(s, m * n, dtype)
+        comb = DeviceBuffer.zeroed(s, m * n, dtype) if res else None
+        _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k,
+                                      dres.ptr if res else None, out.ptr,
+                                      comb.ptr if res else None, dt, _lib.PATH_AUTO, wp, wb))
+        outs.append((out.to_host_vec(s), comb.to_host_vec(s) if res else None))
+    for o, c in outs[1:]:
+        assert np.array_equal(o.view(np.uint8), outs[0][0].view(np.uint8))
+        if res:
+            assert np.array_equal(c, outs[0][1])
+    acc, of, ob = oracle.linear(q, asc, w, ws, k, threads=8)
+    got = outs[0][0]
+    if dtype == np.int32:
+        assert np.array_equal(got, acc)
+    elif dtype == np.uint16:
+        assert np.array_equal(got, ob)
+        want = (bits(oracle.residual(resid, of)) >> 16).astype(np.uint16)
+        assert np.array_equal(outs[0][1], want)
+    else:
+        assert np.array_equal(bits(got), bits(of))
+
+
+def test_linear_split_k_graph_replay(env):
+    """The module's split-K workspace under graph capture: replays reuse the
+    slabs and equal the eager result every time."""
+    ctx, mod, s = env
+    m, n, k = 129, 4096, 12288
+    rng = np.random.default_rng(5150)
+    q = dev(s, rng.integers(-127, 128, (m, k), dtype=np.int8))
+    w = dev(s, rng.integers(-127, 128, (n, k), dtype=np.int8))
+    asc = dev(s, (rng.random(m) / 64 + 1e-4).astype(F32))
+    ws = dev(s, (rng.random(n) / 64 + 1e-4).astype(F32))
+    out = DeviceBuffer.zeroed(s, m * n, np.float32)
+    mod.linear(s, None, q, asc, w, ws, k, out)     # eager: sizes the workspace
+    want = out.to_host_vec(s).copy()
+    g = Graph(s)
+    with g:
+        mod.linear(s, None, q, asc, w, ws, k, out)
+    for rep in range(3):
+        out.fill_zero(s)
+        s.synchronize()
+        g.launch()
+        s.synchronize()
+        assert np.array_equal(bits(out.to_host_vec(s)), bits(want)), f"replay {rep}"
