@@ -7,15 +7,19 @@
 //   :918-930, :1008-1033, :1123-1140, :1249-1288:
 //   out[r][c] = bf(RN(RN(f32(sum_k q[r][k] w[c][k]) * asc[r]) * ws[c]))
 //
-// gfx950 design.  The matrix core op is v_mfma_i32_16x16x64_i8: per lane a
-// 16-byte A fragment (row lane%16) and a 16-byte B fragment (column
-// lane%16), both taken at k offset (lane/16)*16 within the 64-wide step.
-// Any k permutation applied identically to A and B leaves the exact integer
-// sum unchanged, so both operands are read with the same lane -> k map; the
-// 4 x i32 result of lane l holds rows 4*(l/16)+v, column l%16.
+// gfx950 design.  Any k permutation applied identically to A and B leaves
+// the exact integer sum unchanged, so each kernel reads both operands with
+// one lane -> k map of its own choosing.  Layouts of the two matrix-core
+// ops used:
+//   v_mfma_i32_16x16x64_i8: per lane a 16-byte A fragment (row lane%16) and
+//     a 16-byte B fragment (column lane%16); the 4 x i32 result of lane l
+//     holds rows 4*(l/16)+v, column l%16.
+//   v_mfma_i32_32x32x32_i8: 16-byte fragments, row / column lane%32; the
+//     16 x i32 result of lane l holds rows 8*(v/4)+4*(l/32)+v%4, column l%32.
 //
-// Three kernels:
-//  * gemm_dma (M > 64, k % 128 == 0): the prefill GEMM, built on
+// Kernels:
+//  * gemm_dma (M > 64, and 8 <= M <= 64 when n gives >= 128 tiles of 128
+//    columns; k % 128 == 0): the prefill GEMM, built on
 //    v_mfma_i32_32x32x32_i8 (on gfx950 the 16x16x64 int8 form issues at half
 //    its rate), eight waves per workgroup (two per SIMD, so one wave's LDS
 //    reads overlap the other's MFMAs).  Operands move global -> LDS with
@@ -23,17 +27,20 @@
 //    cache lines) through an S-stage ring, one barrier per stage; the
 //    16-byte chunks of each LDS row are XOR-swizzled so fragment reads are
 //    bank-conflict free.  Workgroups are numbered XCD-aware (below).  Tile
-//    shape per problem is chosen by the host from the tile count.
-//  * gemm_skinny (M <= 64, HBM-bound): one workgroup owns 16 weight rows;
-//    its S waves split K and stream their weight fragments straight from
-//    HBM into MFMA B operands (no LDS round trip), activation fragments come
-//    from L1/L2.  Partial i32 tiles are summed through LDS -- exact.
-//  * gemm_tiled (M > 64 with k % 128 != 0): BM x BN output tile, 4 waves, 128-byte K stages
-//    double-buffered in LDS (row pitch 144 B: a 16-lane ds_read_b128 column
-//    touches every bank once), global loads of stage k+1 in flight while
-//    stage k feeds the MFMAs.  Workgroups are numbered so that the M tiles
-//    sharing one weight panel run on the same XCD (workgroup id mod 8 picks
-//    the XCD), so the panel is fetched into that XCD's L2 once.
+//    shape per problem is chosen by the host from the tile count.  With a
+//    caller workspace, some shapes run split-K (i32 slabs + splitk_epilogue).
+//  * gemm_skinny (small M on narrow n, HBM-bound, 16x16x64 MFMA): one
+//    workgroup owns 16 weight rows; its S waves split K and stream their
+//    weight fragments straight from HBM into MFMA B operands (no LDS round
+//    trip), activation fragments come from L1/L2.  Partial i32 tiles are
+//    summed through LDS -- exact.
+//  * gemm_tiled (M > 64 with k % 128 != 0): BM x BN output tile, 4 waves,
+//    128-byte K stages double-buffered in LDS (row pitch 144 B: a 16-lane
+//    ds_read_b128 column touches every bank once), global loads of stage
+//    k+1 in flight while stage k feeds the MFMAs.  Workgroups are numbered
+//    so that the M tiles sharing one weight panel run on the same XCD
+//    (workgroup id mod 8 picks the XCD), so the panel is fetched into that
+//    XCD's L2 once.
 #include <algorithm>
 
 #include "device_common.hpp"
