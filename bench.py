@@ -156,9 +156,14 @@ def main() -> int:
 
     ctx = CudaContext(0)
     cu, arch = ctx.info()
+    clock_mhz = ctx.clock_khz() / 1e3
     mod = load(ctx)
     s = ctx.new_stream()
-    log(f"device {arch} with {cu} CUs")
+    # dense INT8 MFMA peak re-derived from the reported clock: CUs x 4 SIMDs x
+    # 2048 ops/clk (v_mfma_i32_32x32x32_i8: 65536 ops in 32 cycles per SIMD)
+    int8_peak_derived = cu * 4 * 2048 * clock_mhz * 1e6 / 1e12
+    log(f"device {arch} with {cu} CUs at {clock_mhz:.0f} MHz peak; "
+        f"INT8 MFMA peak {int8_peak_derived:.0f} TOPS derived, {INT8_PEAK_TOPS:.0f} published")
 
     # ------------------------------------------------------------ weights
     t0 = time.time()
@@ -401,6 +406,9 @@ def main() -> int:
                             "per_shape": shp}
             log(f"prefill M={m}: {pre[f'M{m}']}")
         extras["prefill"] = pre
+        extras["int8_peak"] = {"published_TOPS": INT8_PEAK_TOPS, "derived_TOPS": round(int8_peak_derived, 1),
+                               "cu": cu, "peak_clock_MHz": round(clock_mhz, 1),
+                               "derivation": "CUs x 4 SIMDs x 2048 ops/clk x peak engine clock"}
         # ragged small batches (config 5): dot4 GEMV vs MFMA GEMM
         rag = {}
         for m in (1, 2, 4, 8, 16, 32, 64):

@@ -70,6 +70,9 @@ int w8a8_init(int device);
 int w8a8_device_count(int *count);
 /* number of compute units and arch name of the current device */
 int w8a8_device_info(int *cu_count, char *arch_name, size_t arch_len);
+/* peak engine clock of the current device in kHz, as the driver reports it
+ * (for deriving the matrix-core peak: CUs x 4 SIMDs x ops/clk x clock) */
+int w8a8_device_clock_khz(int *khz);
 /* ctx.new_stream() (src/gpu.rs:249); *stream receives a hipStream_t */
 int w8a8_stream_create(void **stream);
 int w8a8_stream_destroy(void *stream);

@@ -29,6 +29,7 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_init": (I, [I]),
     "w8a8_device_count": (I, [P]),
     "w8a8_device_info": (I, [P, ctypes.c_char_p, S]),
+    "w8a8_device_clock_khz": (I, [P]),
     "w8a8_stream_create": (I, [P]),
     "w8a8_stream_destroy": (I, [P]),
     "w8a8_stream_synchronize": (I, [P]),

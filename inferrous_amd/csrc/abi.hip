@@ -153,6 +153,16 @@ int w8a8_init(int device) {
   return W8A8_OK;
 }
 
+int w8a8_device_clock_khz(int* khz) {
+  if (!khz) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  e = hipDeviceGetAttribute(khz, hipDeviceAttributeClockRate, dev);
+  return hip_status(e);
+}
+
 int w8a8_device_info(int* cu_count, char* arch_name, size_t arch_len) {
   if (!ready()) return W8A8_EINIT;
   int dev = 0;

@@ -83,6 +83,12 @@ class CudaContext:
         check(lib().w8a8_device_info(ctypes.byref(cu), name, 64), "device info")
         return cu.value, name.value.decode()
 
+    def clock_khz(self) -> int:
+        """Peak engine clock reported by the driver (kHz)."""
+        k = ctypes.c_int()
+        check(lib().w8a8_device_clock_khz(ctypes.byref(k)), "device clock")
+        return k.value
+
 
 def device_count() -> int:
     c = ctypes.c_int()
