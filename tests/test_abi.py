@@ -128,6 +128,55 @@ def test_other_ops_validation():
     assert L.w8a8_init(0) == _lib.ENODEV
 
 
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_fused_and_workspace_entries_validation():
+    L = _lib.lib()
+    F32, BF16, I32 = _lib.OUT_F32, _lib.OUT_BF16, _lib.OUT_I32
+    # swiglu: dtype, empty no-op, nulls, alignment
+    assert L.w8a8_swiglu(None, A, A, 1, 12288, A, A, BF16) == _lib.EINIT
+    assert L.w8a8_swiglu(None, A, A, 1, 12288, A, A, I32) == _lib.EARG
+    assert L.w8a8_swiglu(None, A, A, 0, 12288, A, A, F32) == _lib.OK
+    assert L.w8a8_swiglu(None, A, None, 1, 12288, A, A, F32) == _lib.ENULL
+    assert L.w8a8_swiglu(None, A, A, 1, 12288, A + 2, A, F32) == _lib.EALIGN
+    assert L.w8a8_swiglu(None, A, A, 1, 12288, A, A + 2, BF16) == _lib.EALIGN
+    # linear_swiglu(q, asc, m, k, w_gate, ws_gate, w_up, ws_up, n, gate, up, act, maxima, dtype)
+    sw = lambda **kw: L.w8a8_linear_swiglu(  # noqa: E731
+        None, kw.get("q", A), A, kw.get("m", 1), kw.get("k", 4096), A, A, kw.get("wu", A), A,
+        kw.get("n", 12288), A, A, kw.get("act", A), kw.get("maxima", A), kw.get("dtype", F32))
+    assert sw() == _lib.EINIT
+    assert sw(dtype=I32) == _lib.EARG
+    assert sw(k=4095) == _lib.ESHAPE
+    assert sw(wu=None) == _lib.ENULL
+    assert sw(act=None) == _lib.ENULL
+    assert sw(act=A + 2) == _lib.EALIGN
+    assert sw(maxima=A + 1) == _lib.EALIGN
+    assert sw(m=0) == _lib.OK and sw(n=0) == _lib.OK
+    # linear_quantize_with_max(x, maxima, m, k, q, scales, w, ws, n, residual, out, combined, dtype)
+    qm = lambda **kw: L.w8a8_linear_quantize_with_max(  # noqa: E731
+        None, kw.get("x", A), kw.get("maxima", A), kw.get("m", 1), 12288, A, A, A, A, 4096,
+        kw.get("res"), A, kw.get("comb"), kw.get("dtype", BF16))
+    assert qm() == _lib.EINIT
+    assert qm(x=None) == _lib.ENULL
+    assert qm(maxima=None) == _lib.ENULL
+    assert qm(x=A + 4) == _lib.EALIGN
+    assert qm(res=A) == _lib.ENULL                   # residual without combined
+    assert qm(res=A, comb=A, dtype=I32) == _lib.EARG
+    assert qm(res=A, comb=A) == _lib.EINIT
+    assert qm(m=0) == _lib.OK
+    # linear_ex: the split-K workspace is optional, never required
+    assert L.w8a8_linear_workspace_bytes(1, 4096, 12288) == 0      # dot4 path: none
+    assert L.w8a8_linear_workspace_bytes(512, 4096, 12288) > 0     # 128x128 split in two
+    assert L.w8a8_linear_workspace_bytes(512, 4096, 12288) == 2 * 512 * 4096 * 4
+    ex = lambda **kw: L.w8a8_linear_ex(  # noqa: E731
+        None, A, A, kw.get("m", 512), A, A, 4096, 12288, None, A, None, F32,
+        kw.get("path", _lib.PATH_AUTO), kw.get("wsp", A), kw.get("wsb", 1 << 24))
+    assert ex() == _lib.EINIT
+    assert ex(wsp=None, wsb=0) == _lib.EINIT
+    assert ex(wsb=16) == _lib.EINIT                   # too small: runs unsplit
+    assert ex(wsp=A + 8) == _lib.EALIGN
+    assert ex(path=9) == _lib.EARG
+
+
 def test_module_requires_library_not_oracle():
     """The product package never imports the oracle."""
     for py in (ROOT / "inferrous_amd").rglob("*.py"):
