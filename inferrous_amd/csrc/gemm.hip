@@ -24,11 +24,12 @@
 //    its rate), eight waves per workgroup (two per SIMD, so one wave's LDS
 //    reads overlap the other's MFMAs).  Operands move global -> LDS with
 //    global_load_lds_dwordx4 (no VGPR staging) in 128-byte K stages (whole
-//    cache lines) through an S-stage ring, one barrier per stage; the
-//    16-byte chunks of each LDS row are XOR-swizzled so fragment reads are
-//    bank-conflict free.  Workgroups are numbered XCD-aware (below).  Tile
-//    shape per problem is chosen by the host from the tile count.  With a
-//    caller workspace, some shapes run split-K (i32 slabs + splitk_epilogue).
+//    cache lines) through two rings, activations and weights, the weights
+//    requested further ahead; one barrier per stage; the 16-byte chunks of
+//    each LDS row are XOR-swizzled so fragment reads spread over the banks.
+//    Workgroups are numbered XCD-aware (below).  Tile shape per problem is
+//    chosen by the host from the tile count.  With a caller workspace, some
+//    shapes run split-K (i32 slabs + splitk_epilogue).
 //  * gemm_skinny (small M on narrow n, HBM-bound, 16x16x64 MFMA): one
 //    workgroup owns 16 weight rows; its S waves split K and stream their
 //    weight fragments straight from HBM into MFMA B operands (no LDS round
@@ -266,26 +267,39 @@ __device__ __forceinline__ void store_ep(const GemmArgs& a, uint32_t r, uint32_t
 // Prefill GEMM.  Workgroup = 8 waves (two per SIMD: while one wave waits on
 // LDS the other keeps the matrix core busy), output tile BM x BN, wave tile
 // WM x WN built from 32x32 MFMA blocks.  K advances in 128-byte stages, so
-// every DMA row request is one whole 128-byte cache line.  A stage holds BM
-// activation rows then BN weight rows, 128 bytes each; 16-byte chunk c of LDS
-// row r sits at chunk c ^ (r & 7), so the fragment reads of eight
-// consecutive rows hit eight different 16-byte bank groups.  Sub-step i of a
-// stage covers k bytes [32i, 32i + 32): lane l (row / column l % 32,
-// half h = l / 32) reads chunk 2i + h -- the same lane -> k map for A and B.
-// S stages form a ring; stage kt + S is loaded into stage kt's slot once
-// every wave has finished reading it (one barrier per stage).
-template <int BM, int BN, int WM, int WN, int S, int EP>
+// every DMA row request is one whole 128-byte cache line.
+//
+// LDS holds two rings: activations (A, BM rows of 128 bytes per stage, SA
+// slots) and weights (B, BN rows, SB >= SA slots).  Weight lines mostly miss
+// L2, so they can be requested further ahead than the activation lines,
+// which every workgroup shares.  Batch(kt) = {A(kt + SA - 1), B(kt + SB - 1)}
+// is issued during stage kt (A first) into the slots stage kt - 1 released.
+// Loads complete in issue order, so at the end of stage kt "A(kt + 1) and
+// B(kt + 1) have landed" means: at most the loads issued after A(kt + 1)
+// remain -- the B half of its batch when SB > SA (when SB == SA that half is
+// B(kt + 1) itself and must land too), plus the SA - 2 whole batches after
+// it.
+//
+// 16-byte chunk c of LDS row r sits at chunk c ^ ((r >> 1) & 7): sixteen
+// consecutive rows (two per 256-byte bank window) of one fragment read then
+// hit sixteen different 16-byte bank groups.  Sub-step i of a stage covers
+// k bytes [32i, 32i + 32): lane l (row / column l % 32, half h = l / 32)
+// reads chunk 2i + h -- the same lane -> k map for A and B.
+template <int BM, int BN, int WM, int WN, int SA, int SB, int EP>
 __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, uint32_t tiles_n,
                                                 uint32_t splits) {
   constexpr int WAVES_N = BN / WN;
   static_assert((BM / WM) * (BN / WN) == 8, "eight waves per workgroup");
-  static_assert(WM % 32 == 0 && WN % 32 == 0 && S >= 2 && S <= 4, "tile shape");
+  static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % 64 == 0 && BN % 64 == 0, "tile shape");
+  static_assert(SA >= 2 && SB >= SA && SB >= 3 && SB <= 8, "ring depths");
   constexpr int FM = WM / 32, FN = WN / 32;
-  constexpr int NR = BM + BN;    // LDS rows per stage
-  constexpr int STAGE = NR * 128;
-  static_assert(NR % 64 == 0, "1 KiB DMA blocks (8 rows) divide among the eight waves");
-  constexpr int L = NR / 64;     // DMA loads per wave per stage
-  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+  constexpr int LA = BM / 64, LB = BN / 64;  // DMA loads (8 rows x 128 B) per wave per stage
+  constexpr int L = LA + LB;
+  constexpr int ASL = BM * 128, BSL = BN * 128;
+  static_assert(SA * ASL + SB * BSL <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[SA * ASL + SB * BSL];
+  int8_t* const ldsA = lds;
+  int8_t* const ldsB = lds + SA * ASL;
 
   // Split-K (splits > 1, EP_I32 only): workgroup (tile, split) sums K range
   // [split * K / splits, (split + 1) * K / splits) into i32 slab `split` of
@@ -303,40 +317,60 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   const size_t kbase = (size_t)split * KT * 128;
   if (EP == EP_I32) a.out = reinterpret_cast<int32_t*>(a.out) + (size_t)split * a.m * a.n;
 
-  // Sources of this wave's DMA blocks; rows past M / N re-read row 0 (their
-  // products only reach accumulator cells that are never stored).
-  const int8_t* src[L];
+  // Sources of this wave's DMA loads (8 rows each); rows past M / N re-read
+  // row 0 (their products only reach accumulator cells that are never
+  // stored).  Lane l fills LDS chunk l % 8 of row l / 8 with global chunk
+  // (l % 8) ^ key(row).
+  const int8_t* srcA[LA];
+  const int8_t* srcB[LB];
 #pragma unroll
-  for (int j = 0; j < L; ++j) {
-    const int row = 8 * (wave * L + j) + (lane >> 3);
-    const int gc = (lane & 7) ^ (row & 7);
-    const bool isA = row < BM;
-    const uint32_t g = isA ? m0 + row : n0 + (row - BM);
-    const uint32_t lim = isA ? a.m : a.n;
-    src[j] = (isA ? a.q : a.w) + (size_t)(g < lim ? g : 0) * K + kbase + gc * 16;
+  for (int j = 0; j < LA; ++j) {
+    const int row = 8 * (wave * LA + j) + (lane >> 3);
+    const uint32_t g = m0 + row;
+    srcA[j] = a.q + (size_t)(g < a.m ? g : 0) * K + kbase + ((lane & 7) ^ ((row >> 1) & 7)) * 16;
   }
-  auto issue = [&](uint32_t kt) {
-    int8_t* base = lds + (kt % S) * STAGE;
 #pragma unroll
-    for (int j = 0; j < L; ++j)
-      __builtin_amdgcn_global_load_lds((const void*)(src[j] + (size_t)kt * 128),
-                                       W8A8_LDS_PTR(base + (wave * L + j) * 1024 + lane * 16), 16, 0, 0);
+  for (int j = 0; j < LB; ++j) {
+    const int row = 8 * (wave * LB + j) + (lane >> 3);
+    const uint32_t g = n0 + row;
+    srcB[j] = a.w + (size_t)(g < a.n ? g : 0) * K + kbase + ((lane & 7) ^ ((row >> 1) & 7)) * 16;
+  }
+  auto loadA = [&](uint32_t kt, int j) {
+    __builtin_amdgcn_global_load_lds((const void*)(srcA[j] + (size_t)kt * 128),
+                                     W8A8_LDS_PTR(ldsA + (kt % SA) * ASL + (wave * LA + j) * 1024 + lane * 16),
+                                     16, 0, 0);
   };
+  auto loadB = [&](uint32_t kt, int j) {
+    __builtin_amdgcn_global_load_lds((const void*)(srcB[j] + (size_t)kt * 128),
+                                     W8A8_LDS_PTR(ldsB + (kt % SB) * BSL + (wave * LB + j) * 1024 + lane * 16),
+                                     16, 0, 0);
+  };
+  // Batch(kt), A first.
+  auto batch = [&](uint32_t kt) {
+    if (kt + SA - 1 < KT)
+#pragma unroll
+      for (int j = 0; j < LA; ++j) loadA(kt + SA - 1, j);
+    if (kt + SB - 1 < KT)
+#pragma unroll
+      for (int j = 0; j < LB; ++j) loadB(kt + SB - 1, j);
+  };
+
   const int fr = lane & 31, fh = lane >> 5;
   int off[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) off[i] = fr * 128 + (((2 * i + fh) ^ (fr & 7)) * 16);
+  for (int i = 0; i < 4; ++i) off[i] = fr * 128 + (((2 * i + fh) ^ ((fr >> 1) & 7)) * 16);
   v16i acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
   auto rd = [&](uint32_t kt, int i, v4i (&af)[FM], v4i (&bf)[FN]) {
-    const int8_t* base = lds + (kt % S) * STAGE;
+    const int8_t* ba = ldsA + (kt % SA) * ASL;
+    const int8_t* bb = ldsB + (kt % SB) * BSL;
 #pragma unroll
-    for (int f = 0; f < FM; ++f) af[f] = *(const v4i*)(base + (wm0 + 32 * f) * 128 + off[i]);
+    for (int f = 0; f < FM; ++f) af[f] = *(const v4i*)(ba + (wm0 + 32 * f) * 128 + off[i]);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(base + (BM + wn0 + 32 * j) * 128 + off[i]);
+    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(bb + (wn0 + 32 * j) * 128 + off[i]);
   };
   auto mm = [&](const v4i (&af)[FM], const v4i (&bf)[FN]) {
 #pragma unroll
@@ -344,21 +378,23 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[f][j] = mfma32(af[f], bf[j], acc[f][j]);
   };
-  // This wave's part of stage s has landed once at most (newer stages issued) x L
-  // DMA loads remain outstanding; loads complete in issue order.
-  auto wait_landed = [&](uint32_t newer) {
-    if (newer >= 3) wait_vmcnt<3 * L>();
-    else if (newer == 2) wait_vmcnt<2 * L>();
-    else if (newer == 1) wait_vmcnt<L>();
-    else wait_vmcnt<0>();
-  };
 
+  // Prologue: stages 0 .. SB - 2 (A only up to SA - 2), stage by stage, A
+  // before B; then wait for stage 0.
 #pragma unroll
-  for (int s = 0; s < S; ++s)
-    if (s < (int)KT) issue(s);
-  v4i a0[FM], b0[FN], a1[FM], b1[FN];
-  wait_landed(min(KT - 1, (uint32_t)S - 1));
+  for (int s = 0; s < SB - 1; ++s) {
+    if (s >= (int)KT) break;
+    if (s < SA - 1)
+#pragma unroll
+      for (int j = 0; j < LA; ++j) loadA(s, j);
+#pragma unroll
+    for (int j = 0; j < LB; ++j) loadB(s, j);
+  }
+  if (KT >= (uint32_t)SB - 1) wait_vmcnt<(SA - 2) * LA + (SB - 2) * LB>();
+  else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
+  v4i a0[FM], b0[FN], a1[FM], b1[FN];
+  batch(0);
   rd(0, 0, a0, b0);
   // Fragments of the next sub-step are read while the current one's MFMAs
   // run.  The loop body has no branch between a read and its use, so the
@@ -370,11 +406,13 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
     mm(a1, b1);
     rd(kt, 3, a1, b1);
     mm(a0, b0);
-    // stages issued so far: 0 .. min(KT - 1, kt + S - 1); stage kt + 1 must have landed
-    wait_landed(min(KT - 1, kt + S - 1) - (kt + 1));
+    // A(kt + 1), B(kt + 1) landed (every load counted here exists while batch
+    // kt was complete)
+    if (kt + SB - 1 < KT) wait_vmcnt<(SB > SA ? LB : 0) + (SA - 2) * L>();
+    else wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of stage kt returned
     __builtin_amdgcn_s_barrier();         // all waves: stage kt + 1 landed, stage kt read
-    if (kt + S < KT) issue(kt + S);       // into stage kt's slot
+    batch(kt + 1);                        // into the slots stage kt released
     rd(kt + 1, 0, a0, b0);
     mm(a1, b1);
   }
@@ -401,20 +439,20 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   }
 }
 
-template <int BM, int BN, int WM, int WN, int S>
+template <int BM, int BN, int WM, int WN, int SA, int SB>
 static void launch_dma(hipStream_t st, const GemmArgs& a) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
   const dim3 grid(tm * tn), block(512);
   if (a.out_dtype == W8A8_OUT_I32)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_I32>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32>), grid, block, 0, st, a, tm, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32_RES>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32_RES>), grid, block, 0, st, a, tm, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_F32>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32>), grid, block, 0, st, a, tm, tn, 1u);
   else if (a.residual)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16_RES>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16_RES>), grid, block, 0, st, a, tm, tn, 1u);
   else
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_BF16>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16>), grid, block, 0, st, a, tm, tn, 1u);
 }
 
 // Split-K epilogue: out[r][c] = epilogue(sum over slabs of partials[s][r][c]).
@@ -460,13 +498,13 @@ size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
   return (size_t)splits * m * n * sizeof(int32_t);
 }
 
-template <int BM, int BN, int WM, int WN, int S>
+template <int BM, int BN, int WM, int WN, int SA, int SB>
 static hipError_t launch_split(hipStream_t st, const GemmArgs& a, uint32_t splits) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
   GemmArgs p = a;
   p.out = a.partials;
   p.out_dtype = W8A8_OUT_I32;
-  hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, S, EP_I32>), dim3(tm * tn * splits), dim3(512), 0, st, p,
+  hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32>), dim3(tm * tn * splits), dim3(512), 0, st, p,
                      tm, tn, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -506,23 +544,23 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
     uint32_t splits;
     if (a.partials && split_plan(a.m, a.n, a.k, tile, splits) &&
         a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))
-      return tile == 0 ? launch_split<128, 128, 32, 64, 4>(st, a, splits)
-                       : launch_split<128, 64, 32, 32, 4>(st, a, splits);
+      return tile == 0 ? launch_split<128, 128, 32, 64, 4, 4>(st, a, splits)
+                       : launch_split<128, 64, 32, 32, 4, 4>(st, a, splits);
     // Tile per problem, measured on MI355X at M = 129 / 512 on the Qwen3-8B
     // projection shapes: the largest tile that still gives about one tile
     // per CU, smaller tiles for narrow N.
     const uint64_t t256 = (uint64_t)((a.m + 255) / 256) * ((a.n + 191) / 192);
     const uint64_t t128 = (uint64_t)((a.m + 127) / 128) * ((a.n + 191) / 192);
     if (t256 >= 240)
-      launch_dma<256, 192, 64, 96, 2>(st, a);
+      launch_dma<256, 192, 64, 96, 2, 3>(st, a);
     else if (t128 >= 240)
-      launch_dma<128, 192, 32, 96, 3>(st, a);
+      launch_dma<128, 192, 32, 96, 2, 4>(st, a);
     else if (a.n >= 6144 && a.m >= 256)
-      launch_dma<128, 128, 32, 64, 4>(st, a);
+      launch_dma<128, 128, 32, 64, 4, 4>(st, a);
     else if (a.m >= 128)
-      launch_dma<128, 64, 32, 32, 4>(st, a);
+      launch_dma<128, 64, 32, 32, 4, 4>(st, a);
     else
-      launch_dma<64, 128, 32, 32, 4>(st, a);
+      launch_dma<64, 128, 32, 32, 4, 4>(st, a);
   } else {
     constexpr int BM = 128, BN = 128;
     const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
