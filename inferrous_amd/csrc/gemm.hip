@@ -456,20 +456,25 @@ static void launch_dma(hipStream_t st, const GemmArgs& a) {
 }
 
 // Split-K epilogue: out[r][c] = epilogue(sum over slabs of partials[s][r][c]).
-// The i32 sum is exact in any order.  Four columns per thread.
+// The i32 sum is exact in any order.  blockIdx.y walks rows (the row scale is
+// one scalar load), each thread four consecutive columns (n % 4 == 0), so the
+// slab, weight-scale and residual loads are all issued up front.
 template <int EP>
 __global__ __launch_bounds__(256) void splitk_epilogue(GemmArgs a, const int32_t* __restrict__ partials,
                                                         uint32_t splits) {
   const size_t mn = (size_t)a.m * a.n;
-  for (size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4; i < mn; i += (size_t)gridDim.x * 1024) {
+  const uint32_t c = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= a.n) return;
+  float wsc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (EP != EP_I32)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wsc[j] = a.ws[c + j];
+  for (uint32_t r = blockIdx.y; r < a.m; r += gridDim.y) {
+    const size_t i = (size_t)r * a.n + c;
     v4i acc = *reinterpret_cast<const v4i*>(partials + i);
     for (uint32_t s = 1; s < splits; ++s) acc += *reinterpret_cast<const v4i*>(partials + s * mn + i);
-    const uint32_t r = (uint32_t)(i / a.n), c = (uint32_t)(i % a.n);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float wsc = EP != EP_I32 ? a.ws[c + j] : 0.f;
-      store_ep<EP>(a, r, c + j, acc[j], wsc);
-    }
+    for (int j = 0; j < 4; ++j) store_ep<EP>(a, r, c + j, acc[j], wsc[j]);
   }
 }
 
@@ -508,18 +513,17 @@ static hipError_t launch_split(hipStream_t st, const GemmArgs& a, uint32_t split
                      tm, tn, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t mn = (size_t)a.m * a.n;
-  const unsigned blocks = (unsigned)std::min<size_t>((mn / 4 + 255) / 256, 4096);
+  const dim3 grid((a.n / 4 + 255) / 256, std::min<uint32_t>(a.m, 65535));
   if (a.out_dtype == W8A8_OUT_I32)
-    hipLaunchKernelGGL(splitk_epilogue<EP_I32>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL(splitk_epilogue<EP_I32>, grid, dim3(256), 0, st, a, a.partials, splits);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    hipLaunchKernelGGL(splitk_epilogue<EP_F32_RES>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL(splitk_epilogue<EP_F32_RES>, grid, dim3(256), 0, st, a, a.partials, splits);
   else if (a.out_dtype == W8A8_OUT_F32)
-    hipLaunchKernelGGL(splitk_epilogue<EP_F32>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL(splitk_epilogue<EP_F32>, grid, dim3(256), 0, st, a, a.partials, splits);
   else if (a.residual)
-    hipLaunchKernelGGL(splitk_epilogue<EP_BF16_RES>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL(splitk_epilogue<EP_BF16_RES>, grid, dim3(256), 0, st, a, a.partials, splits);
   else
-    hipLaunchKernelGGL(splitk_epilogue<EP_BF16>, dim3(blocks), dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL(splitk_epilogue<EP_BF16>, grid, dim3(256), 0, st, a, a.partials, splits);
   return hipGetLastError();
 }
 
