@@ -336,6 +336,9 @@ def main() -> int:
         ubuf = DeviceBuffer.zeroed(s, ffn, np.float32)
         act = DeviceBuffer.zeroed(s, ffn, np.float32)
         comb = DeviceBuffer.zeroed(s, 4096, np.uint16)
+        gains = [DeviceBuffer.from_host(s, (1 + 0.1 * synth.normal_rows(44 + i, 1, 4096)).astype(np.float32)
+                                        .reshape(-1)) for i in range(2)]
+        normed = DeviceBuffer.zeroed(s, 4096, np.float32)
         q4, sc4 = qs[4096]
         q12, sc12 = qs[12288]
         halves = []
@@ -348,11 +351,11 @@ def main() -> int:
         def layer_chain():
             for mats, (wg_, sg_, wu_, su_) in zip(layers, halves):
                 (_, _, _, wqkv, sqkv), (_, _, _, wo, so), _, (_, _, _, wd, sd) = mats
-                mod.quantize(s, None, xs[4096], 4096, q4, sc4, maxima_reset=mx)
+                mod.norm_quantize(s, None, xs[4096], gains[0], normed, q4, sc4, mx)
                 mod.linear(s, None, q4, sc4, wqkv, sqkv, 4096, outs["qkv"])
                 mod.quantize(s, None, xs[4096], 4096, q4, sc4)
                 mod.linear_residual(s, None, q4, sc4, wo, so, 4096, resid, outs["o"], comb)
-                mod.quantize(s, None, xs[4096], 4096, q4, sc4, maxima_reset=mx)
+                mod.norm_quantize(s, None, xs[4096], gains[1], normed, q4, sc4, mx)
                 mod.linear_swiglu(s, None, q4, sc4, 4096, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx)
                 mod.linear_quantize_with_max(s, None, act, ffn, mx, q12, sc12, wd, sd, outs["down"],
                                              resid, comb)
@@ -365,8 +368,24 @@ def main() -> int:
         extras["decode_reference_chain"] = {
             "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
             "launches": 8 * synth.LAYERS + 3,
-            "chain": "quantize, qkv, quantize, o+residual, quantize, linear_swiglu, quantize_with_max, down+residual; lm_head"}
+            "chain": "norm_quantize, qkv, quantize, o+residual, norm_quantize, linear_swiglu, quantize_with_max, down+residual; lm_head"}
         log(f"reference decode chain: {ms * 1e3:.1f} us ({extras['decode_reference_chain']['GB/s']} GB/s)")
+        # latency-bound producers at M = 1: per call in a graph of 100
+        # stream-ordered calls (launch gap included)
+        act12 = DeviceBuffer.from_host(s, synth.normal_rows(45, 1, ffn).reshape(-1))
+        lat_ops = {
+            "quantize_4096": lambda: mod.quantize(s, None, xs[4096], 4096, q4, sc4),
+            "quantize_with_max_12288": lambda: mod.quantize_with_max(s, None, act12, ffn, mx, q12, sc12),
+            "norm_quantize_4096": lambda: mod.norm_quantize(s, None, xs[4096], gains[0], normed, q4, sc4, mx),
+        }
+        lat = {}
+        for name, fn in lat_ops.items():
+            def hundred(fn=fn):
+                for _ in range(100):
+                    fn()
+            lat[name] = round(time_graph(capture(hundred), 5) / 100 * 1e3, 2)
+        extras["producer_us_per_call"] = lat
+        log(f"producers (us per call in a graph): {lat}")
         # prefill (config 4): M = 512 TOPS and M = 129 HBM GB/s, 36 layers x 4 shapes
         pre = {}
         for m in (512, 129):

@@ -127,6 +127,21 @@ int w8a8_quantize_with_max(void *stream, const float *x, uint32_t width,
                            size_t rows, const uint32_t *maxima, int8_t *q,
                            float *scales);
 
+/* `norm_quantize` (src/kernels.rs:476-575; host wrapper src/gpu.rs:340-363,
+ * decode call sites src/gpu.rs:552, :713): RMSNorm of each 4096-wide row of
+ * x[rows, 4096] with gain[4096], then the row's quantization:
+ *   sum = the reference's sum tree of RN(x^2) (src/kernels.rs:354-392);
+ *   inv = 1 / sqrt(RN(RN(sum / 4096) + 1e-6));
+ *   out_j = bf(RN(RN(x_j * inv) * gain_j))        (f32 holding BF16 values)
+ *   (q, scales) = quantize(out);  maxima[r] = bits(1e-8f).
+ * inv is 1/sqrt in binary64 rounded to binary32; the reference's approximate
+ * rsqrt is not reproduced, so `out` agrees with it within the reference's
+ * tolerance, and q / scales equal w8a8_quantize(out) exactly.  width must be
+ * 4096 (the reference's fixed hidden width). */
+int w8a8_norm_quantize(void *stream, const float *x, const float *gain,
+                       size_t rows, uint32_t width, float *out, int8_t *q,
+                       float *scales, uint32_t *maxima);
+
 /* `linear` (src/kernels.rs:807-845) for any m, and the M>1 GEMMs
  * `linear_prefill` / `linear_splitk` / `linear_tiled` / `linear_large`
  * (src/kernels.rs:846-1289) behind one entry, dispatched as

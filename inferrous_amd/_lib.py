@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_linear_residual": (I, [P, P, P, S, P, P, S, U32, P, P, P, I]),
     "w8a8_linear_grouped": (I, [P, P, P, S, U32, I, P, P, P, P, I]),
     "w8a8_linear_workspace_bytes": (S, [S, S, U32]),
+    "w8a8_norm_quantize": (I, [P, P, P, S, U32, P, P, P, P]),
     "w8a8_linear_ex": (I, [P, P, P, S, P, P, S, U32, P, P, P, I, I, P, S]),
     "w8a8_linear_quantize_with_max": (I, [P, P, P, S, U32, P, P, P, P, S, P, P, P, I]),
     "w8a8_linear_swiglu": (I, [P, P, P, S, U32, P, P, P, P, S, P, P, P, P, I]),

@@ -364,6 +364,18 @@ int w8a8_quantize_with_max(void* stream, const float* x, uint32_t width, size_t 
   return hip_status(launch_quantize_with_max((hipStream_t)stream, x, width, rows, maxima, q, scales));
 }
 
+int w8a8_norm_quantize(void* stream, const float* x, const float* gain, size_t rows, uint32_t width,
+                       float* out, int8_t* q, float* scales, uint32_t* maxima) {
+  if (width != 4096) return W8A8_ESHAPE;
+  if (rows == 0) return W8A8_OK;
+  if (rows > kU32Max) return W8A8_ESHAPE;
+  if (!x || !gain || !out || !q || !scales || !maxima) return W8A8_ENULL;
+  if (!al(x, 4) || !al(gain, 4) || !al(out, 4) || !al(scales, 4) || !al(maxima, 4))
+    return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_norm_quantize((hipStream_t)stream, x, gain, rows, out, q, scales, maxima));
+}
+
 int w8a8_linear_path(void* stream, const int8_t* q, const float* asc, size_t m, const int8_t* w,
                      const float* ws, size_t n, uint32_t k, void* out, int out_dtype, int path) {
   if (path != W8A8_PATH_AUTO && path != W8A8_PATH_DOT4 && path != W8A8_PATH_MFMA) return W8A8_EARG;

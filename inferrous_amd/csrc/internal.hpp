@@ -70,6 +70,8 @@ hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t wi
 hipError_t launch_quantize_with_max(hipStream_t st, const float* x, uint32_t width, size_t rows,
                                     const uint32_t* maxima, int8_t* q, float* scales);
 hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8_t* out);
+hipError_t launch_norm_quantize(hipStream_t st, const float* x, const float* gain, size_t rows,
+                                float* out, int8_t* q, float* scales, uint32_t* maxima);  // width 4096
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);

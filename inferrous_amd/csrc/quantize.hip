@@ -3,7 +3,8 @@
 // Reference semantics (crates/inferrous-qwen3/):
 //   quantize           src/kernels.rs:414-452
 //   quantize_with_max  src/kernels.rs:453-475
-//   norm_quantize tail src/kernels.rs:547-575 (maxima reset at :566)
+//   norm_quantize      src/kernels.rs:476-575 (sum tree of `norm` :354-392,
+//                      maxima reset at :566)
 //   rounding_probe     src/kernels.rs:325-333
 //
 // MI355X design: one 256-thread workgroup (4 waves) per token row.  Each
@@ -196,6 +197,68 @@ __global__ __launch_bounds__(256) void rounding_probe_kernel(const float* __rest
 }
 
 // ------------------------------------------------------------------ launchers
+// RMSNorm of one 4096-wide row per workgroup, then the row's quantization.
+// The sum of squares keeps the reference's order exactly: thread t sums
+// RN(x^2) over coordinates t + 256 i (i = 0..15, sequential RN adds), then
+// the halving tree p[t] = RN(p[t] + p[t + d]), d = 128, 64, ..., 1 -- here
+// the first two levels in one wave from LDS, the rest with wave shuffles
+// (lane 0 only consumes in-range partners).  inv = 1 / sqrt(mean + 1e-6)
+// is evaluated in binary64 and rounded once to binary32; the reference uses
+// an approximate rsqrt (src/kernels.rs:5-6), so `out` matches it within its
+// tolerance, while (q, scale) are exactly the quantization of `out`.
+__global__ __launch_bounds__(256) void norm_quantize_4096(
+    const float* __restrict__ x, const float* __restrict__ gain, float* __restrict__ out,
+    int8_t* __restrict__ q, float* __restrict__ scales, uint32_t* __restrict__ maxima) {
+  __shared__ float part[256];
+  __shared__ float inv_shared;
+  __shared__ uint32_t red[4];
+  const size_t r = blockIdx.x;
+  const int t = threadIdx.x;
+  const float* row = x + r * 4096;
+  float v[16], g[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    v[i] = row[t + 256 * i];
+    g[i] = gain[t + 256 * i];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s = s + v[i] * v[i];
+  part[t] = s;
+  __syncthreads();
+  if (t < 64) {
+    float a = part[t] + part[t + 128];           // d = 128 (t < 64)
+    const float b = part[t + 64] + part[t + 192];  // d = 128 (t + 64 < 128)
+    a = a + b;                                   // d = 64
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) a = a + __shfl_down(a, d, kWave);
+    if (t == 0) {
+      const float m = a / 4096.0f + 1e-6f;  // RN division, RN add
+      inv_shared = (float)(1.0 / __builtin_sqrt((double)m));
+    }
+  }
+  __syncthreads();
+  const float inv = inv_shared;
+  float* orow = out + r * 4096;
+  uint32_t mb = kFloorBits;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float o = bf16_rne((v[i] * inv) * g[i]);
+    v[i] = o;
+    orow[t + 256 * i] = o;
+    mb = max(mb, abs_bits_no_nan(o));
+  }
+  mb = block_max_256(mb, red);
+  const float sc = __uint_as_float(mb) / 127.0f;
+  int8_t* qrow = q + r * 4096;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) qrow[t + 256 * i] = round_i8(v[i] / sc);
+  if (t == 0) {
+    scales[r] = sc;
+    maxima[r] = kFloorBits;
+  }
+}
+
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t width, size_t rows,
@@ -229,6 +292,19 @@ hipError_t launch_quantize_with_max(hipStream_t st, const float* x, uint32_t wid
                        0, st, x, width, total, maxima, q, scales);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_norm_quantize(hipStream_t st, const float* x, const float* gain, size_t rows,
+                                float* out, int8_t* q, float* scales, uint32_t* maxima) {
+  constexpr size_t kChunk = size_t(1) << 30;  // rows per launch (grid x limit)
+  for (size_t r0 = 0; r0 < rows; r0 += kChunk) {
+    const size_t n = rows - r0 < kChunk ? rows - r0 : kChunk;
+    hipLaunchKernelGGL(norm_quantize_4096, dim3((unsigned)n), dim3(256), 0, st, x + r0 * 4096, gain,
+                       out + r0 * 4096, q + r0 * 4096, scales + r0, maxima + r0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8_t* out) {

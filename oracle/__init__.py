@@ -57,6 +57,9 @@ def lib() -> ctypes.CDLL:
             "orc_residual": (None, [P, P, S, P]),
             "orc_silu_mul": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
             "orc_swiglu": (ctypes.c_uint32, [P, P, S, P]),
+            "orc_norm_sum_sq": (ctypes.c_float, [P]),
+            "orc_norm_rows": (None, [P, P, S, P]),
+            "orc_norm_quantize": (None, [P, P, S, P, P, P, P]),
             "orc_argmax": (ctypes.c_uint32, [P, S]),
             "orc_linear_argmax": (ctypes.c_uint32, [P, P, P, P, S, S, P, ctypes.c_int]),
             "orc_mix64": (U64, [U64]),
@@ -187,6 +190,36 @@ def swiglu(gate, up):
     act = np.empty(g.size, np.float32)
     mx = int(lib().orc_swiglu(_p(g), _p(u), g.size, _p(act)))
     return act, mx
+
+
+def norm_sum_sq(x) -> float:
+    """The reference's sum-of-squares tree for one 4096-wide row
+    (src/kernels.rs:354-392)."""
+    x = _c(x, np.float32).reshape(-1)
+    assert x.size == 4096
+    return float(lib().orc_norm_sum_sq(_p(x)))
+
+
+def norm_rows(x, gain):
+    """`norm` at width 4096 (src/kernels.rs:347-402); rsqrt in binary64."""
+    x = _c(x, np.float32).reshape(-1, 4096)
+    g = _c(gain, np.float32).reshape(4096)
+    out = np.empty_like(x)
+    lib().orc_norm_rows(_p(x), _p(g), x.shape[0], _p(out))
+    return out
+
+
+def norm_quantize(x, gain):
+    """(out, q, scales, maxima) of `norm_quantize` (src/kernels.rs:476-575)."""
+    x = _c(x, np.float32).reshape(-1, 4096)
+    g = _c(gain, np.float32).reshape(4096)
+    rows = x.shape[0]
+    out = np.empty_like(x)
+    q = np.empty((rows, 4096), np.int8)
+    s = np.empty(rows, np.float32)
+    mx = np.empty(rows, np.uint32)
+    lib().orc_norm_quantize(_p(x), _p(g), rows, _p(out), _p(q), _p(s), _p(mx))
+    return out, q, s, mx
 
 
 def argmax(x) -> int:

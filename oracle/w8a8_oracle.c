@@ -200,6 +200,47 @@ uint32_t orc_swiglu(const float *gate, const float *up, size_t n, float *act) {
   return orc_absmax_bits(act, n); /* fold(1e-8, max |act|), NaN ignored */
 }
 
+/* src/kernels.rs:354-392: 256 partial sums, each a sequential RN sum over
+ * the thread's 16 coordinates (stride 256), then the halving tree. */
+float orc_norm_sum_sq(const float *x) {
+  float p[256];
+  for (int t = 0; t < 256; ++t) {
+    float s = 0.0f;
+    for (int i = 0; i < 16; ++i) {
+      const float v = x[t + 256 * i];
+      s = s + v * v; /* RN multiply, then RN add (-ffp-contract=off) */
+    }
+    p[t] = s;
+  }
+  for (int d = 128; d > 0; d /= 2)
+    for (int t = 0; t < d; ++t) p[t] = p[t] + p[t + d];
+  return p[0];
+}
+
+static float norm_inv(const float *x) {
+  const float mean = orc_norm_sum_sq(x) / 4096.0f; /* RN division */
+  const float a = mean + 1e-6f;                    /* RN add */
+  return (float)(1.0 / sqrt((double)a));
+}
+
+void orc_norm_rows(const float *x, const float *gain, size_t rows, float *out) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float *row = x + r * 4096;
+    const float inv = norm_inv(row);
+    for (int j = 0; j < 4096; ++j) {
+      const float a = row[j] * inv;
+      out[r * 4096 + j] = orc_bf16_rne(a * gain[j]);
+    }
+  }
+}
+
+void orc_norm_quantize(const float *x, const float *gain, size_t rows,
+                       float *out, int8_t *q, float *scales, uint32_t *maxima) {
+  orc_norm_rows(x, gain, rows, out);
+  orc_quantize_rows(out, rows, 4096, q, scales);
+  for (size_t r = 0; r < rows; ++r) maxima[r] = f2u(1e-8f);
+}
+
 /* src/kernels.rs:2196-2229: scan with (v > best) || (v == best && i < idx);
  * a sequential ascending scan with strict '>' keeps the lowest index, and
  * IEEE '==' makes -0 and +0 tie (src/model.rs:210-215). */

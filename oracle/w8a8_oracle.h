@@ -80,6 +80,22 @@ float orc_silu_mul(float g, float u);
  * (src/conformance.rs:596-603). */
 uint32_t orc_swiglu(const float *gate, const float *up, size_t n, float *act);
 
+/* src/kernels.rs:347-393 `norm` (hidden width 4096) and src/kernels.rs:476-575
+ * `norm_quantize`, which keeps norm's BF16 boundary and sum tree:
+ *   p[t] = sequential RN sum of RN(x[t + 256 i]^2), i = 0..15, t = 0..255;
+ *   halving tree p[t] = RN(p[t] + p[t + d]), d = 128, 64, ..., 1;
+ *   inv = rsqrt(RN(RN(p[0] / 4096) + 1e-6));
+ *   out_j = bf(RN(RN(x_j * inv) * gain_j));
+ *   (q, scale) = quantize(out) (src/kernels.rs:414-452); maxima = bits(1e-8).
+ * The reference's rsqrt is NVIDIA's approximate rsqrt (src/kernels.rs:5-6),
+ * which is not reproduced: here inv is 1/sqrt evaluated in IEEE binary64 and
+ * rounded to binary32, so `out` is compared with the reference within its
+ * tolerance, and (q, scale) equal quantize(out) exactly. */
+float orc_norm_sum_sq(const float *x); /* the tree sum p[0] of one row */
+void orc_norm_rows(const float *x, const float *gain, size_t rows, float *out);
+void orc_norm_quantize(const float *x, const float *gain, size_t rows,
+                       float *out, int8_t *q, float *scales, uint32_t *maxima);
+
 /* src/kernels.rs:2191-2231 `select_token` (equal to src/model.rs:206-218
  * `argmax` when that returns Ok): largest value, lowest index on ties,
  * -0 == +0; empty input or any non-finite value -> 0xFFFFFFFF. */

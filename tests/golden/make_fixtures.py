@@ -20,6 +20,13 @@ generator (bitemyapp/inferrous, crates/inferrous-qwen3/tools/operator_fixtures.p
   src/conformance.rs:663).  The reference draws its rope/attention inputs
   before this case; those draws are not repeated, so ``up`` differs from the
   reference's own file while following the same recipe.
+* norm (tools/operator_fixtures.py:36-40) at width 4096, the width of
+  `norm_quantize` (src/kernels.rs:476-575): x = bf16(randn(3, 4096)) with
+  row 0 zero, gain = bf16(randn(4096)), expected
+  ``out = bf16(x * rsqrt(mean(x^2) + 1e-6) * gain)`` in torch's float32
+  (compared within the reference's tolerance).  Drawn from its own
+  generator (seed 825) after the other cases, so the earlier files keep
+  their bytes.
 * weight_quantize (tools/prepare.py:79-83, offline weight quantization):
   BF16 weights [33, 4096] (row 0 zero, row 1 with +-127 and .5 ties) as BF16
   bits, expected ``scale = amax(|w|, 1).clamp(min=1e-8) / 127`` and
@@ -113,6 +120,13 @@ def main() -> None:
     wscale = wf.abs().amax(1, keepdim=True).clamp(min=1e-8) / 127.0
     wq = torch.round(wf / wscale).clamp(-127, 127).to(torch.int8)
     out.add("weight_quantize", {"w": w.view(torch.int16), "q": wq, "scale": wscale.flatten()})
+
+    gen = torch.Generator().manual_seed(825)
+    x = to_bf16_values(torch.randn(3, 4096, generator=gen))
+    x[0] = 0
+    gain = to_bf16_values(torch.randn(4096, generator=gen))
+    normed = to_bf16_values(x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6) * gain)
+    out.add("norm", {"x": x, "gain": gain, "out": normed}, width=4096)
 
     manifest = {"generator": "tests/golden/make_fixtures.py", "torch": torch.__version__,
                 "seed": 824, "cases": out.cases}

@@ -163,6 +163,15 @@ def test_fused_and_workspace_entries_validation():
     assert qm(res=A, comb=A, dtype=I32) == _lib.EARG
     assert qm(res=A, comb=A) == _lib.EINIT
     assert qm(m=0) == _lib.OK
+    # norm_quantize(x, gain, rows, width, out, q, scales, maxima): width 4096 only
+    nq = lambda **kw: L.w8a8_norm_quantize(  # noqa: E731
+        None, kw.get("x", A), A, kw.get("m", 2), kw.get("width", 4096), kw.get("out", A), A, A,
+        kw.get("maxima", A))
+    assert nq() == _lib.EINIT
+    assert nq(width=4095) == _lib.ESHAPE and nq(width=2048) == _lib.ESHAPE
+    assert nq(m=0) == _lib.OK
+    assert nq(x=None) == _lib.ENULL and nq(maxima=None) == _lib.ENULL
+    assert nq(out=A + 2) == _lib.EALIGN
     # linear_ex: the split-K workspace is optional, never required
     assert L.w8a8_linear_workspace_bytes(1, 4096, 12288) == 0      # dot4 path: none
     assert L.w8a8_linear_workspace_bytes(512, 4096, 12288) > 0     # 128x128 split in two

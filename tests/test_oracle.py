@@ -335,3 +335,84 @@ def test_planted_operand_and_tie_mistakes_are_rejected(fixtures):
     # argmax keeping the last of tied maxima
     x = argmax_cases()[-1]
     assert int(x.size - 1 - np.argmax(x[::-1])) != oracle.argmax(x)
+
+
+# ------------------------------------------------------------------ norm_quantize
+def _tree_sum_numpy(row: np.ndarray) -> np.float32:
+    """Independent numpy form of the reference's sum tree (src/kernels.rs:354-392):
+    partial t = sequential f32 sum over x[t::256]**2, then p[:d] += p[d:2d]."""
+    sq = (row.astype(np.float32) * row.astype(np.float32)).astype(np.float32).reshape(16, 256)
+    p = np.zeros(256, np.float32)
+    for i in range(16):
+        p = (p + sq[i]).astype(np.float32)
+    d = 128
+    while d:
+        p[:d] = (p[:d] + p[d:2 * d]).astype(np.float32)
+        d //= 2
+    return p[0]
+
+
+def test_norm_sum_tree_order_is_pinned():
+    rng = np.random.default_rng(71)
+    rows = (rng.standard_normal((8, 4096)) * np.exp(rng.uniform(-6, 6, (8, 4096)))).astype(np.float32)
+    differs = 0
+    for row in rows:
+        got = oracle.norm_sum_sq(row)
+        assert np.float32(got) == _tree_sum_numpy(row)
+        seq = np.float32(0)
+        for v in row:
+            seq = np.float32(seq + np.float32(v * v))
+        differs += np.float32(got) != seq
+        assert abs(got - float(np.sum(row.astype(np.float64) ** 2))) <= 1e-5 * float(np.sum(row.astype(np.float64) ** 2))
+    assert differs > 0, "inputs must distinguish the tree from a sequential sum"
+
+
+def test_norm_sum_exact_on_representable_squares():
+    rng = np.random.default_rng(72)
+    row = rng.choice(np.array([-3, -2, -1, -0.5, 0, 0.5, 1, 2, 3], np.float32), 4096)
+    assert oracle.norm_sum_sq(row) == float(np.sum(row.astype(np.float64) ** 2))
+
+
+def test_norm_quantize_kats():
+    gain = np.ones(4096, np.float32)
+    # all ones: mean 1, inv = 1/sqrt(f32(1 + 1e-6)) -> out rounds to BF16 1.0, q = 127
+    out, q, s, mx = oracle.norm_quantize(np.ones((1, 4096), np.float32), gain)
+    assert np.all(out == 1.0) and np.all(q == 127)
+    assert s[0] == np.float32(1.0) / np.float32(127.0) and mx[0] == int(np.float32(1e-8).view(np.uint32))
+    # zero row: out 0, q 0, scale at the 1e-8 floor
+    out, q, s, _ = oracle.norm_quantize(np.zeros((1, 4096), np.float32), gain)
+    assert np.all(out == 0) and np.all(q == 0) and s[0] == np.float32(1e-8) / np.float32(127.0)
+    # a NaN anywhere: every output NaN, quantized to 0
+    x = np.ones((1, 4096), np.float32)
+    x[0, 7] = np.nan
+    out, q, s, _ = oracle.norm_quantize(x, gain)
+    assert np.isnan(out).all() and np.all(q == 0)
+
+
+def test_norm_against_float64_and_fixture(fixtures):
+    (case,) = fixtures.cases("norm")
+    x, gain, want = (fixtures.tensor(case, k) for k in ("x", "gain", "out"))
+    got = oracle.norm_rows(x, gain)
+    assert reference_tolerance_ok(got, want)
+    assert np.all(got[0] == 0)
+    rng = np.random.default_rng(73)
+    x = (rng.standard_normal((5, 4096)) * [[1e-3], [1], [30], [1e3], [1]]).astype(np.float32)
+    g = (1 + 0.25 * rng.standard_normal(4096)).astype(np.float32)
+    got = oracle.norm_rows(x, g)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-6) * g
+    # one BF16 rounding (at most 2^-8 of the value) plus the f32 steps before
+    # it; the 1e-3 row has mean(x^2) = 1e-6, where the epsilon halves 1/rms
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7.95)
+
+
+def test_norm_quantize_equals_norm_then_quantize():
+    """src/conformance.rs:166-199: the fused operator equals `norm`, then `quantize`."""
+    rng = np.random.default_rng(74)
+    x = rng.standard_normal((4, 4096)).astype(np.float32)
+    g = rng.standard_normal(4096).astype(np.float32)
+    out, q, s, mx = oracle.norm_quantize(x, g)
+    assert np.array_equal(out, oracle.norm_rows(x, g))
+    q2, s2 = oracle.quantize(out, 4096)
+    assert np.array_equal(q.reshape(-1), q2) and np.array_equal(s, s2)
+    assert np.all(mx == np.float32(1e-8).view(np.uint32))
