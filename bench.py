@@ -386,6 +386,39 @@ def main() -> int:
             lat[name] = round(time_graph(capture(hundred), 5) / 100 * 1e3, 2)
         extras["producer_us_per_call"] = lat
         log(f"producers (us per call in a graph): {lat}")
+        # the reference model's own head: BF16 151936 x 4096, losslessly packed
+        # (src/kernels.rs:2258-2373), then select_token.  4096 distinct rows of
+        # N(0, 0.02) weights are packed on the host and the packed rows are
+        # replicated on the device up to the vocabulary (every row streams
+        # from HBM; the exception list is shared, so offsets repeat).
+        from inferrous_amd import PackedBf16
+        from inferrous_amd import _lib as L
+        base_rows = 4096
+        wbase = (np.random.default_rng(46).standard_normal((base_rows, 4096)).astype(np.float32)
+                 * np.float32(0.02)).view(np.uint32) >> 16
+        pk = PackedBf16.new(wbase.astype(np.uint16))
+        words = DeviceBuffer.zeroed(s, hn * 1536, np.uint32)
+        wb = DeviceBuffer.from_host(s, pk.words)
+        for r0 in range(0, hn, base_rows):
+            nr = min(base_rows, hn - r0)
+            L.check(L.lib().w8a8_memcpy_dtod(words.ptr + r0 * 1536 * 4, wb.ptr, nr * 1536 * 4, s.handle))
+        offs = DeviceBuffer.from_host(s, np.tile(pk.offsets.reshape(base_rows, 16), (hn // base_rows + 1, 1))[:hn]
+                                      .reshape(-1))
+        exc = DeviceBuffer.from_host(s, pk.exceptions)
+        hx = DeviceBuffer.from_host(s, synth.normal_rows(47, 1, 4096).reshape(-1))
+        logits = DeviceBuffer.zeroed(s, hn, np.float32)
+        s.synchronize()
+        head_bytes = hn * 1536 * 4 + hn * 16 * 4 + 4096 * 4 + hn * 4
+        t_head = time_graph(capture(lambda: mod.head_packed(s, None, hx, words, offs, exc, logits)), 20)
+        t_sel = time_graph(capture(lambda: (mod.head_packed(s, None, hx, words, offs, exc, logits),
+                                            mod.select_token(s, None, logits, token))), 20)
+        extras["bf16_packed_head"] = {
+            "us": round(t_head * 1e3, 2), "GB/s": round(head_bytes / (t_head * 1e-3) / 1e9, 1),
+            "pct_hbm_peak": round(head_bytes / (t_head * 1e-3) / 1e9 / HBM_PEAK_GBS * 100, 2),
+            "us_with_select_token": round(t_sel * 1e3, 2), "bytes": head_bytes,
+            "escapes_per_value": round(pk.exceptions.size / wbase.size, 4),
+            "reference_us": 574.0, "reference_hw": "RTX PRO 6000 Blackwell Max-Q, docs/qwen3-8b-w8a8/optimization/round-6.md:14"}
+        log(f"packed BF16 head: {extras['bf16_packed_head']}")
         # prefill (config 4): M = 512 TOPS and M = 129 HBM GB/s, 36 layers x 4 shapes
         pre = {}
         for m in (512, 129):

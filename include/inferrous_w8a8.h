@@ -142,6 +142,36 @@ int w8a8_norm_quantize(void *stream, const float *x, const float *gain,
                        size_t rows, uint32_t width, float *out, int8_t *q,
                        float *scales, uint32_t *maxima);
 
+/* The reference's BF16 lm_head, stored losslessly packed.
+ *
+ * w8a8_bf16_pack (host only; `PackedBf16::new`, src/packing.rs:8-46): codes n
+ * BF16 values (n % 256 == 0) into words[n / 8 * 3], offsets[n / 256] and
+ * exceptions[*exceptions_len] (at most n, at least 1 entry; capacity
+ * exceptions_cap).  A value whose exponent is in [109, 124) takes 12 bits;
+ * others escape to the chunk's exception list.  Lossless for every BF16
+ * pattern.
+ *
+ * w8a8_head_packed (`head_packed`, src/kernels.rs:2258-2373; host call site
+ * src/gpu.rs:800-810): exceptions_len is the packer's *exceptions_len (it
+ * bounds the last chunk's list).  Logits out[r] for rows of 4096 packed values against
+ * the last 4096 values of x (x_len >= 4096; that row 16-byte aligned), with
+ * the reference's FP32 order:
+ * 32 lane sums over j = l, l + 32, ... then the halving tree; out = bf(sum).
+ * Bit-identical to the unpacked `head` (src/kernels.rs:2233-2257).
+ *
+ * w8a8_unpack_bf16 (`unpack_head`, src/kernels.rs:2376-2388): the n values
+ * back as BF16 bits. */
+int w8a8_bf16_pack(const uint16_t *in, size_t n, uint32_t *words,
+                   uint32_t *offsets, uint16_t *exceptions,
+                   size_t exceptions_cap, size_t *exceptions_len);
+int w8a8_head_packed(void *stream, const float *x, size_t x_len,
+                     const uint32_t *words, const uint32_t *offsets,
+                     const uint16_t *exceptions, size_t exceptions_len,
+                     size_t rows, float *out);
+int w8a8_unpack_bf16(void *stream, const uint32_t *words,
+                     const uint32_t *offsets, const uint16_t *exceptions,
+                     size_t n, uint16_t *out);
+
 /* `linear` (src/kernels.rs:807-845) for any m, and the M>1 GEMMs
  * `linear_prefill` / `linear_splitk` / `linear_tiled` / `linear_large`
  * (src/kernels.rs:846-1289) behind one entry, dispatched as

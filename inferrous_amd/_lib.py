@@ -60,6 +60,9 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_linear_grouped": (I, [P, P, P, S, U32, I, P, P, P, P, I]),
     "w8a8_linear_workspace_bytes": (S, [S, S, U32]),
     "w8a8_norm_quantize": (I, [P, P, P, S, U32, P, P, P, P]),
+    "w8a8_bf16_pack": (I, [P, S, P, P, P, S, P]),
+    "w8a8_head_packed": (I, [P, P, S, P, P, P, S, S, P]),
+    "w8a8_unpack_bf16": (I, [P, P, P, P, S, P]),
     "w8a8_linear_ex": (I, [P, P, P, S, P, P, S, U32, P, P, P, I, I, P, S]),
     "w8a8_linear_quantize_with_max": (I, [P, P, P, S, U32, P, P, P, P, S, P, P, P, I]),
     "w8a8_linear_swiglu": (I, [P, P, P, S, U32, P, P, P, P, S, P, P, P, P, I]),

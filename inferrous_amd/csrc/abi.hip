@@ -376,6 +376,49 @@ int w8a8_norm_quantize(void* stream, const float* x, const float* gain, size_t r
   return hip_status(launch_norm_quantize((hipStream_t)stream, x, gain, rows, out, q, scales, maxima));
 }
 
+int w8a8_bf16_pack(const uint16_t* in, size_t n, uint32_t* words, uint32_t* offsets,
+                   uint16_t* exceptions, size_t exceptions_cap, size_t* exceptions_len) {
+  if (n % 256 != 0 || n > kU32Max) return W8A8_ESHAPE;
+  if (!exceptions_len) return W8A8_ENULL;
+  if (n > 0 && (!in || !words || !offsets)) return W8A8_ENULL;
+  if (!exceptions) return W8A8_ENULL;
+  // worst case: every value escapes (and the list holds at least one entry)
+  size_t need = 1;
+  for (size_t i = 0; i < n; ++i) {
+    const uint32_t e = (in[i] >> 7) & 255u;
+    need += (e < 109u || e >= 124u);
+  }
+  if (need > 1) --need;
+  if (exceptions_cap < need) return W8A8_EWORKSPACE;
+  *exceptions_len = pack_bf16_host(in, n, words, offsets, exceptions);
+  return W8A8_OK;
+}
+
+int w8a8_head_packed(void* stream, const float* x, size_t x_len, const uint32_t* words,
+                     const uint32_t* offsets, const uint16_t* exceptions, size_t exceptions_len,
+                     size_t rows, float* out) {
+  if (x_len < 4096 || rows > kU32Max / 16 || exceptions_len == 0 || exceptions_len > kU32Max)
+    return W8A8_ESHAPE;
+  if (rows == 0) return W8A8_OK;
+  if (!x || !words || !offsets || !exceptions || !out) return W8A8_ENULL;
+  if (!al(x + (x_len - 4096), 16) || !al(words, 4) || !al(offsets, 4) || !al(exceptions, 2) ||
+      !al(out, 4))
+    return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_head_packed((hipStream_t)stream, x + (x_len - 4096), words, offsets, exceptions,
+                                       (uint32_t)exceptions_len, (uint32_t)rows, out));
+}
+
+int w8a8_unpack_bf16(void* stream, const uint32_t* words, const uint32_t* offsets,
+                     const uint16_t* exceptions, size_t n, uint16_t* out) {
+  if (n % 256 != 0) return W8A8_ESHAPE;
+  if (n == 0) return W8A8_OK;
+  if (!words || !offsets || !exceptions || !out) return W8A8_ENULL;
+  if (!al(words, 4) || !al(offsets, 4) || !al(exceptions, 2) || !al(out, 2)) return W8A8_EALIGN;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_unpack_bf16((hipStream_t)stream, words, offsets, exceptions, n, out));
+}
+
 int w8a8_linear_path(void* stream, const int8_t* q, const float* asc, size_t m, const int8_t* w,
                      const float* ws, size_t n, uint32_t k, void* out, int out_dtype, int path) {
   if (path != W8A8_PATH_AUTO && path != W8A8_PATH_DOT4 && path != W8A8_PATH_MFMA) return W8A8_EARG;

@@ -70,6 +70,13 @@ hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t wi
 hipError_t launch_quantize_with_max(hipStream_t st, const float* x, uint32_t width, size_t rows,
                                     const uint32_t* maxima, int8_t* q, float* scales);
 hipError_t launch_rounding_probe(hipStream_t st, const float* in, size_t n, int8_t* out);
+hipError_t launch_head_packed(hipStream_t st, const float* x4096, const uint32_t* words,
+                              const uint32_t* offsets, const uint16_t* exceptions, uint32_t n_exceptions,
+                              uint32_t rows, float* out);
+hipError_t launch_unpack_bf16(hipStream_t st, const uint32_t* words, const uint32_t* offsets,
+                              const uint16_t* exceptions, size_t n, uint16_t* out);
+size_t pack_bf16_host(const uint16_t* in, size_t n, uint32_t* words, uint32_t* offsets,
+                      uint16_t* exceptions);
 hipError_t launch_norm_quantize(hipStream_t st, const float* x, const float* gain, size_t rows,
                                 float* out, int8_t* q, float* scales, uint32_t* maxima);  // width 4096
 

@@ -58,6 +58,9 @@ def lib() -> ctypes.CDLL:
             "orc_silu_mul": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
             "orc_swiglu": (ctypes.c_uint32, [P, P, S, P]),
             "orc_norm_sum_sq": (ctypes.c_float, [P]),
+            "orc_bf16_pack": (S, [P, S, P, P, P]),
+            "orc_bf16_unpack_at": (ctypes.c_uint16, [P, P, P, S]),
+            "orc_head_bf16": (None, [P, P, S, P]),
             "orc_norm_rows": (None, [P, P, S, P]),
             "orc_norm_quantize": (None, [P, P, S, P, P, P, P]),
             "orc_argmax": (ctypes.c_uint32, [P, S]),
@@ -220,6 +223,34 @@ def norm_quantize(x, gain):
     mx = np.empty(rows, np.uint32)
     lib().orc_norm_quantize(_p(x), _p(g), rows, _p(out), _p(q), _p(s), _p(mx))
     return out, q, s, mx
+
+
+def bf16_pack(values):
+    """src/packing.rs:8-46: (words u32, offsets u32, exceptions u16)."""
+    v = _c(values, np.uint16).reshape(-1)
+    assert v.size % 256 == 0
+    words = np.empty(v.size // 8 * 3, np.uint32)
+    offsets = np.empty(v.size // 256, np.uint32)
+    exc = np.empty(max(v.size, 1), np.uint16)
+    n = int(lib().orc_bf16_pack(_p(v), v.size, _p(words), _p(offsets), _p(exc)))
+    return words, offsets, exc[:n].copy()
+
+
+def bf16_unpack_at(words, offsets, exceptions, i: int) -> int:
+    words = _c(words, np.uint32)
+    offsets = _c(offsets, np.uint32)
+    exceptions = _c(exceptions, np.uint16)
+    return int(lib().orc_bf16_unpack_at(_p(words), _p(offsets), _p(exceptions), i))
+
+
+def head_bf16(x, w_bits):
+    """`head` (src/kernels.rs:2233-2257): x's last 4096 values against BF16
+    rows [rows, 4096]; f32 logits holding BF16 values."""
+    x = _c(x, np.float32).reshape(-1)[-4096:].copy()
+    w = _c(w_bits, np.uint16).reshape(-1, 4096)
+    out = np.empty(w.shape[0], np.float32)
+    lib().orc_head_bf16(_p(x), _p(w), w.shape[0], _p(out))
+    return out
 
 
 def argmax(x) -> int:

@@ -241,6 +241,63 @@ void orc_norm_quantize(const float *x, const float *gain, size_t rows,
   for (size_t r = 0; r < rows; ++r) maxima[r] = f2u(1e-8f);
 }
 
+size_t orc_bf16_pack(const uint16_t *in, size_t n, uint32_t *words,
+                     uint32_t *offsets, uint16_t *exceptions) {
+  size_t nexc = 0;
+  memset(words, 0, n / 8 * 3 * sizeof(uint32_t));
+  for (size_t c = 0; c < n / 256; ++c) {
+    const size_t base = nexc;
+    offsets[c] = (uint32_t)base;
+    for (size_t local = 0; local < 256; ++local) {
+      const uint16_t v = in[c * 256 + local];
+      const uint32_t e = (v >> 7) & 255u;
+      uint32_t code;
+      if (e >= 109 && e < 124) {
+        code = ((e - 109) << 8) | ((v >> 8) & 128u) | (v & 127u);
+      } else {
+        code = 0xf00u | (uint32_t)(nexc - base);
+        exceptions[nexc++] = v;
+      }
+      const size_t step = local / 32; /* which of the lane's eight codes */
+      const size_t word = c * 96 + local % 32 + (step * 12 / 32) * 32;
+      const unsigned shift = (unsigned)(step * 12 % 32);
+      words[word] |= code << shift;
+      if (shift > 20) words[word + 32] |= code >> (32 - shift);
+    }
+  }
+  if (nexc == 0) exceptions[nexc++] = 0; /* keep the list nonempty */
+  return nexc;
+}
+
+uint16_t orc_bf16_unpack_at(const uint32_t *words, const uint32_t *offsets,
+                            const uint16_t *exceptions, size_t i) {
+  const size_t step = i % 256 / 32;
+  const size_t word = i / 256 * 96 + i % 32 + (step * 12 / 32) * 32;
+  const unsigned shift = (unsigned)(step * 12 % 32);
+  uint32_t code = words[word] >> shift;
+  if (shift > 20) code |= words[word + 32] << (32 - shift);
+  code &= 4095u;
+  if (code >> 8 == 15) return exceptions[offsets[i / 256] + (code & 255u)];
+  return (uint16_t)(((code & 128u) << 8) | (((code >> 8) + 109u) << 7) | (code & 127u));
+}
+
+void orc_head_bf16(const float *x4096, const uint16_t *w, size_t rows, float *out) {
+  for (size_t r = 0; r < rows; ++r) {
+    float lane[32];
+    for (int l = 0; l < 32; ++l) {
+      float s = 0.0f;
+      for (int j = l; j < 4096; j += 32) {
+        const float wv = u2f((uint32_t)w[r * 4096 + j] << 16);
+        s = s + x4096[j] * wv;
+      }
+      lane[l] = s;
+    }
+    for (int d = 16; d > 0; d /= 2)
+      for (int l = 0; l < d; ++l) lane[l] = lane[l] + lane[l + d];
+    out[r] = orc_bf16_rne(lane[0]);
+  }
+}
+
 /* src/kernels.rs:2196-2229: scan with (v > best) || (v == best && i < idx);
  * a sequential ascending scan with strict '>' keeps the lowest index, and
  * IEEE '==' makes -0 and +0 tie (src/model.rs:210-215). */

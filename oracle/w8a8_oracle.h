@@ -96,6 +96,24 @@ void orc_norm_rows(const float *x, const float *gain, size_t rows, float *out);
 void orc_norm_quantize(const float *x, const float *gain, size_t rows,
                        float *out, int8_t *q, float *scales, uint32_t *maxima);
 
+/* src/packing.rs:8-46 `PackedBf16::new`: lossless 12-bit coding of BF16 values
+ * in 256-value chunks.  Exponents 109..123 code as ((e - 109) << 8) | sign << 7
+ * | mantissa; anything else escapes to 0xF00 | index into the chunk's
+ * exception list.  32 lane streams of eight codes, interleaved in 96 words
+ * per chunk.  n % 256 == 0; words[n/8*3], offsets[n/256], exceptions[<= n]
+ * (at least one entry).  Returns the number of exceptions written. */
+size_t orc_bf16_pack(const uint16_t *in, size_t n, uint32_t *words,
+                     uint32_t *offsets, uint16_t *exceptions);
+/* src/kernels.rs:295-314 `unpack_code` / `unpack_bf16`: value i. */
+uint16_t orc_bf16_unpack_at(const uint32_t *words, const uint32_t *offsets,
+                            const uint16_t *exceptions, size_t i);
+/* src/kernels.rs:2233-2257 `head` (= `head_packed` :2258-2373 bit for bit):
+ * for each row, 32 lane sums, lane l the sequential RN sum of
+ * RN(x[j] * w[row][j]) over j = l, l + 32, ..., then the halving tree over the
+ * 32 lanes (d = 16 .. 1); out = bf(sum).  x is the last 4096 values of the
+ * activation; w is BF16 bits [rows, 4096]. */
+void orc_head_bf16(const float *x4096, const uint16_t *w, size_t rows, float *out);
+
 /* src/kernels.rs:2191-2231 `select_token` (equal to src/model.rs:206-218
  * `argmax` when that returns Ok): largest value, lowest index on ties,
  * -0 == +0; empty input or any non-finite value -> 0xFFFFFFFF. */

@@ -27,6 +27,10 @@ generator (bitemyapp/inferrous, crates/inferrous-qwen3/tools/operator_fixtures.p
   (compared within the reference's tolerance).  Drawn from its own
   generator (seed 825) after the other cases, so the earlier files keep
   their bytes.
+* head (tools/operator_fixtures.py:78-79): x = bf16(randn(3, 4096)),
+  w = BF16 randn(33, 4096) (stored as BF16 bits), expected
+  ``out = bf16(x[-1:] @ w.T)`` in torch's float32 (compared within the
+  reference's tolerance).  Own generator (seed 826), drawn last.
 * weight_quantize (tools/prepare.py:79-83, offline weight quantization):
   BF16 weights [33, 4096] (row 0 zero, row 1 with +-127 and .5 ties) as BF16
   bits, expected ``scale = amax(|w|, 1).clamp(min=1e-8) / 127`` and
@@ -127,6 +131,12 @@ def main() -> None:
     gain = to_bf16_values(torch.randn(4096, generator=gen))
     normed = to_bf16_values(x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6) * gain)
     out.add("norm", {"x": x, "gain": gain, "out": normed}, width=4096)
+
+    gen = torch.Generator().manual_seed(826)
+    x = to_bf16_values(torch.randn(3, 4096, generator=gen))
+    w = torch.randn(33, 4096, generator=gen).bfloat16()
+    logits = to_bf16_values(x[-1:] @ w.float().T)
+    out.add("head", {"x": x, "w": w.view(torch.int16), "out": logits.flatten()})
 
     manifest = {"generator": "tests/golden/make_fixtures.py", "torch": torch.__version__,
                 "seed": 824, "cases": out.cases}

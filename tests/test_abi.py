@@ -191,3 +191,43 @@ def test_module_requires_library_not_oracle():
     for py in (ROOT / "inferrous_amd").rglob("*.py"):
         text = py.read_text()
         assert "import oracle" not in text and "from oracle" not in text, py
+
+
+def test_bf16_packer_is_host_side_and_matches_oracle():
+    """w8a8_bf16_pack needs no device: the library's packer against the oracle's."""
+    import numpy as np
+
+    import oracle
+    from inferrous_amd import PackedBf16
+    a = np.arange(65536, dtype=np.uint32)
+    rng = np.random.default_rng(9)
+    trained = (rng.standard_normal(4096 * 4).astype(np.float32) * 0.02).view(np.uint32) >> 16
+    v = np.concatenate([a, (a * 40503) % 65536, trained]).astype(np.uint16)
+    p = PackedBf16.new(v)
+    w, o, e = oracle.bf16_pack(v)
+    assert np.array_equal(p.words, w) and np.array_equal(p.offsets, o) and np.array_equal(p.exceptions, e)
+    L = _lib.lib()
+    n = ctypes.c_size_t()
+    buf = np.zeros(512, np.uint32)
+    exc = np.zeros(1, np.uint16)
+    zeros = np.zeros(256, np.uint16)        # every value escapes: capacity 1 is too small
+    assert L.w8a8_bf16_pack(zeros.ctypes.data, 256, buf.ctypes.data, buf.ctypes.data, exc.ctypes.data, 1,
+                            ctypes.byref(n)) == _lib.EWORKSPACE
+    assert L.w8a8_bf16_pack(zeros.ctypes.data, 255, buf.ctypes.data, buf.ctypes.data, exc.ctypes.data, 1,
+                            ctypes.byref(n)) == _lib.ESHAPE
+    assert L.w8a8_bf16_pack(zeros.ctypes.data, 256, buf.ctypes.data, buf.ctypes.data, exc.ctypes.data, 1,
+                            None) == _lib.ENULL
+
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_head_entries_validation():
+    L = _lib.lib()
+    assert L.w8a8_head_packed(None, A, 4096, A, A, A, 1, 33, A) == _lib.EINIT
+    assert L.w8a8_head_packed(None, A, 4095, A, A, A, 1, 33, A) == _lib.ESHAPE
+    assert L.w8a8_head_packed(None, A, 4096, A, A, A, 0, 33, A) == _lib.ESHAPE
+    assert L.w8a8_head_packed(None, A, 4096, A, A, A, 1, 0, A) == _lib.OK
+    assert L.w8a8_head_packed(None, A, 4096, None, A, A, 1, 33, A) == _lib.ENULL
+    assert L.w8a8_head_packed(None, A + 2, 4096, A, A, A, 1, 33, A) == _lib.EALIGN
+    assert L.w8a8_unpack_bf16(None, A, A, A, 256, A) == _lib.EINIT
+    assert L.w8a8_unpack_bf16(None, A, A, A, 255, A) == _lib.ESHAPE
+    assert L.w8a8_unpack_bf16(None, A, A, A, 256, A + 1) == _lib.EALIGN

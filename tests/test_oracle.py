@@ -416,3 +416,90 @@ def test_norm_quantize_equals_norm_then_quantize():
     q2, s2 = oracle.quantize(out, 4096)
     assert np.array_equal(q.reshape(-1), q2) and np.array_equal(s, s2)
     assert np.all(mx == np.float32(1e-8).view(np.uint32))
+
+
+# ------------------------------------------------------------------ packed BF16 head
+def _unpack_all_numpy(words, offsets, exceptions, n):
+    """Independent vectorised decoder of src/kernels.rs:295-314."""
+    i = np.arange(n, dtype=np.int64)
+    step = (i % 256) // 32
+    word = i // 256 * 96 + i % 32 + (step * 12 // 32) * 32
+    shift = (step * 12 % 32).astype(np.uint64)
+    lo = words[word].astype(np.uint64)
+    hi = np.where(word + 32 < words.size, words[np.minimum(word + 32, words.size - 1)], 0).astype(np.uint64)
+    code = ((lo | (hi << np.uint64(32))) >> shift) & np.uint64(4095)
+    code = code.astype(np.int64)
+    direct = ((code & 128) << 8) | (((code >> 8) + 109) << 7) | (code & 127)
+    esc = exceptions[np.minimum(offsets[i // 256].astype(np.int64) + (code & 255), exceptions.size - 1)]
+    return np.where(code >> 8 == 15, esc, direct).astype(np.uint16)
+
+
+def _reference_exhaustive_input():
+    """src/packing.rs tests and src/conformance.rs:716-720: every BF16 pattern,
+    then (i * 40503) mod 2^16 for i < 65536 (mixed chunks)."""
+    a = np.arange(65536, dtype=np.uint32)
+    return np.concatenate([a, (a * 40503) % 65536]).astype(np.uint16)
+
+
+def test_bf16_pack_round_trips_every_pattern():
+    v = _reference_exhaustive_input()
+    words, offsets, exc = oracle.bf16_pack(v)
+    assert np.array_equal(_unpack_all_numpy(words, offsets, exc, v.size), v)
+    for i in range(0, v.size, 4099):
+        assert oracle.bf16_unpack_at(words, offsets, exc, i) == v[i]
+
+
+def test_bf16_pack_format_kats():
+    v = np.zeros(256, np.uint16)
+    v[0] = np.float32(2.0 ** -18).view(np.uint32) >> 16        # exponent 109: direct code 0x000
+    v[1] = (np.float32(-0.1).view(np.uint32) >> 16)            # exponent 123: direct, sign bit
+    v[2] = np.float32(0.125).view(np.uint32) >> 16             # exponent 124: escapes
+    v[32] = 0x3C00                                             # lane 0, second code
+    words, offsets, exc = oracle.bf16_pack(v)
+    assert words.size == 96 and offsets.tolist() == [0]
+    # lane 0's first code sits in bits 0-11 of word 0, its second in bits 12-23
+    assert words[0] & 0xFFF == 0 and (words[0] >> 12) & 0xFFF == ((0x3C00 >> 7 & 255) - 109) << 8
+    assert (words[1] & 0xFFF) == (((v[1] >> 7) & 255) - 109) << 8 | 128 | (v[1] & 127)
+    # 0.125 is the chunk's first escape (index 0); the 252 zeros (exponent 0)
+    # escape after it, in value order -> 253 exceptions
+    assert exc.size == 253 and exc[0] == v[2] and (words[2] & 0xFFF) == 0xF00
+    assert (words[3] & 0xFFF) == 0xF01 and exc[1] == 0
+
+
+def _head_numpy(x4096, w_bits):
+    """Independent numpy statement of src/kernels.rs:2233-2257's order."""
+    w = (w_bits.astype(np.uint32) << 16).view(np.float32).reshape(-1, 4096)
+    x = x4096.astype(np.float32)
+    prod = (x[None, :] * w).astype(np.float32).reshape(w.shape[0], 128, 32)
+    lane = np.zeros((w.shape[0], 32), np.float32)
+    for i in range(128):
+        lane = (lane + prod[:, i, :]).astype(np.float32)
+    d = 16
+    while d:
+        lane[:, :d] = (lane[:, :d] + lane[:, d:2 * d]).astype(np.float32)
+        d //= 2
+    return lane[:, 0]
+
+
+def test_head_order_is_pinned(fixtures):
+    (case,) = fixtures.cases("head")
+    x, w, want = (fixtures.tensor(case, k) for k in ("x", "w", "out"))
+    got = oracle.head_bf16(x, w.view(np.uint16))
+    assert reference_tolerance_ok(got, want)
+    rng = np.random.default_rng(81)
+    x = (rng.standard_normal(4096) * np.exp(rng.uniform(-4, 4, 4096))).astype(np.float32)
+    wb = (rng.standard_normal((64, 4096)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    got = oracle.head_bf16(x, wb)
+    tree = _head_numpy(x, wb)
+    # before the final BF16 rounding the tree sums agree bit for bit
+    assert np.array_equal(got.view(np.uint32), oracle.bf16_rne(tree).view(np.uint32))
+    # the tree sum (before BF16) separates the reference order from a
+    # sequential one on these rows
+    wf = (wb.astype(np.uint32) << 16).view(np.float32)
+    differs = 0
+    for r in range(8):
+        s = np.float32(0)
+        for j in range(4096):
+            s = np.float32(s + np.float32(x[j] * wf[r, j]))
+        differs += s != tree[r]
+    assert differs > 0
