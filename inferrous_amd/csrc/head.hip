@@ -21,14 +21,16 @@
 //
 // MI355X design: one 32-lane half-wave per row, so lane l of the half-wave is
 // the reference's lane l.  Each half-wave issues all 48 of its word loads
-// (6 KiB of row, three contiguous 128-byte segments per chunk) and the 16
+// (6 KiB of row, three contiguous 128-byte segments per chunk) and the
 // exception-list offsets up front; the activation row is staged in LDS once
 // per workgroup and read back with the two halves of a wave hitting the same
-// addresses (broadcast).  Escapes are rare for trained head weights (|w| in
-// [2^-18, 2^-3) codes directly): a chunk whose exception list is empty
-// (offsets[c + 1] == offsets[c], uniform per row) decodes every code with
-// bit operations only; a chunk with escapes tests each code and loads the
-// escaped values.
+// addresses (broadcast).  The kernel is bound by vector-ALU issue, so the
+// decode is held to four instructions per value (plus three shifts per
+// chunk).  Escapes are rare for trained head weights (|w| in [2^-18, 2^-3)
+// codes directly): every code is decoded as if direct, and only in a chunk
+// whose exception list is non-empty (in either row of the wave) is each code
+// position tested -- one ballot per position -- and the escaped values
+// loaded.
 #include <algorithm>
 #include <vector>
 
@@ -49,12 +51,35 @@ __device__ __forceinline__ float unpack_value(uint32_t code, const uint16_t* __r
     bits = ((code & 128u) << 8) | (((code >> 8) + 109u) << 7) | (code & 127u);
   return __uint_as_float(bits << 16);
 }
-
-// A code known not to be an escape, straight to f32 bits: sign from bit 7,
-// exponent (bits 11..8) + 109, mantissa bits 6..0.  Bits above 11 are ignored.
-__device__ __forceinline__ float decode_direct(uint32_t code) {
-  const uint32_t e = ((code >> 8) & 15u) + 109u;
-  return __uint_as_float(((code & 128u) << 24) | (e << 23) | ((code & 127u) << 16));
+// The eight codes of one lane stream (96 bits w2:w1:w0, code t at bits
+// [12t, 12t + 12)), each taken as direct, straight to f32 bits:
+//   B = (exponent nibble + 109) << 23          bit-field extract, shift-add
+//   A = sign/mantissa byte copied to bytes 3, 2 byte permute (sign at bit 31,
+//                                              mantissa at bits 22..16)
+//   f = (A & 0x807F0000) | B                   and-or
+// The sign/mantissa bytes of the odd codes are nibble-aligned; three funnel
+// shifts of the stream by 4 bits make all four byte-aligned.  The
+// instructions are written out so that the compiler keeps this selection
+// (it otherwise re-forms the expressions into five or six operations).
+__device__ __forceinline__ void decode_chunk(uint32_t w0, uint32_t w1, uint32_t w2, float (&v)[8]) {
+  const uint32_t y0 = __builtin_amdgcn_alignbit(w1, w0, 4);  // stream bits 4..35
+  const uint32_t y1 = __builtin_amdgcn_alignbit(w2, w1, 4);  // stream bits 36..67
+  const uint32_t y2 = w2 >> 4;                               // stream bits 68..95
+  const uint32_t smw[8] = {w0, y0, w0, y1, w1, y1, w2, y2};  // word holding code t's sign/mantissa byte
+  constexpr uint32_t smb[8] = {0, 1, 3, 0, 2, 3, 1, 2};      // its byte index there
+  const uint32_t ew[8] = {w0, w0, w1, w1, w1, w2, w2, w2};   // word holding code t's exponent nibble
+  constexpr uint32_t eb[8] = {8, 20, 0, 12, 24, 4, 16, 28};  // its bit offset there
+  const uint32_t cexp = 109u << 23, cmask = 0x807F0000u;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t sel = (smb[t] << 24) | (smb[t] << 16) | 0x0C0Cu;
+    uint32_t e, B, A, f;
+    asm("v_bfe_u32 %0, %1, %2, 4" : "=v"(e) : "v"(ew[t]), "i"(eb[t]));
+    asm("v_lshl_add_u32 %0, %1, 23, %2" : "=v"(B) : "v"(e), "s"(cexp));
+    asm("v_perm_b32 %0, 0, %1, %2" : "=v"(A) : "v"(smw[t]), "s"(sel));
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(f) : "v"(A), "s"(cmask), "v"(B));
+    v[t] = __uint_as_float(f);
+  }
 }
 
 __global__ __launch_bounds__(kHeadThreads) void head_packed_kernel(
@@ -68,9 +93,9 @@ __global__ __launch_bounds__(kHeadThreads) void head_packed_kernel(
   const uint32_t row = blockIdx.x * (kHeadThreads / 32) + (threadIdx.x >> 5);
   const uint32_t r = min(row, rows - 1);  // tail half-waves recompute the last row
   // Loads complete in issue order: first the activation row into LDS (DMA,
-  // 1 KiB per wave instruction), then lane g's exception-list offset of chunk
-  // g (g <= 16), then the 48 words -- so after one wait for the first five
-  // the row's words keep streaming while chunk 0 is decoded.
+  // 1 KiB per wave instruction), then the exception-list offsets, then the
+  // 48 words -- so after one wait for the first five the row's words keep
+  // streaming while chunk 0 is decoded.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int blk = i * 4 + wave;
@@ -100,23 +125,38 @@ __global__ __launch_bounds__(kHeadThreads) void head_packed_kernel(
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   if (past_end) my_off = n_exceptions;
-  uint32_t off[17];
-#pragma unroll
-  for (int g = 0; g <= 16; ++g) off[g] = __shfl(my_off, g, 32);
+  // chunk g has escapes iff offsets[g + 1] != offsets[g]; the mask ORs the
+  // wave's two rows, so every branch below is uniform over the wave
+  const uint32_t o_next = (uint32_t)__shfl_down((int)my_off, 1, 32);
+  const unsigned long long bal = __ballot(lane < 16 && o_next != my_off);
+  const uint32_t wmask = ((uint32_t)bal | (uint32_t)(bal >> 32)) & 0xffffu;
+  const float* xl = xs + lane;
   float sum = 0.f;
 #pragma unroll
   for (int g = 0; g < 16; ++g) {
     const uint32_t w0 = w[g][0], w1 = w[g][1], w2 = w[g][2];
-    const uint32_t code[8] = {w0, w0 >> 12, (w0 >> 24) | (w1 << 8), w1 >> 4,
-                              w1 >> 16, (w1 >> 28) | (w2 << 4), w2 >> 8, w2 >> 20};
-    const float* xg = xs + g * 256 + lane;
-    if (off[g + 1] == off[g]) {  // no escape in this chunk (uniform per row)
+    float xv[8], v[8];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) sum = sum + xg[32 * t] * decode_direct(code[t]);
-    } else {
+    for (int t = 0; t < 8; ++t) xv[t] = xl[g * 256 + 32 * t];
+    decode_chunk(w0, w1, w2, v);
+    if ((wmask >> g) & 1u) {  // rare: replace the escaped codes' values
+      const uint32_t og = (uint32_t)__shfl((int)my_off, g, 32);
+      const uint32_t code[8] = {w0, w0 >> 12, (w0 >> 24) | (w1 << 8), w1 >> 4,
+                                w1 >> 16, (w1 >> 28) | (w2 << 4), w2 >> 8, w2 >> 20};
 #pragma unroll
-      for (int t = 0; t < 8; ++t) sum = sum + xg[32 * t] * unpack_value(code[t], exceptions, off[g]);
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t c = code[t] & 4095u;
+        const bool esc = c >= 0xf00u;
+        if (__ballot(esc) != 0) {
+          if (esc) v[t] = __uint_as_float((uint32_t)exceptions[min(og + (c & 255u), n_exceptions - 1)] << 16);
+        }
+      }
     }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) sum = sum + xv[t] * v[t];
+    // keeps this chunk's products here: left alone, the compiler sinks the
+    // whole sum chain below the last branch and holds all 128 values live
+    asm volatile("" : "+v"(sum));
   }
 #pragma unroll
   for (int d = 16; d > 0; d >>= 1) sum = sum + __shfl_down(sum, d, 32);

@@ -95,3 +95,28 @@ def test_select_over_packed_logits(env):
     mod.select_token(s, None, dev(s, logits), token)
     s.synchronize()
     assert int(token.to_host_vec(s)[0]) == oracle.argmax(oracle.head_bf16(x, w))
+
+
+def test_head_packed_many_rows_mixed_escapes(env):
+    """Enough rows that every workgroup of the persistent grid runs several
+    steps with both register sets, a row count that is not a multiple of 8,
+    and rows of every escape regime side by side (none, up to 32 -- held one
+    per lane --, exactly 32, 33, and most values)."""
+    rng = np.random.default_rng(9)
+    rows = 20011
+    x = oracle.bf16_rne(rng.standard_normal(4096).astype(F32))
+    w = to_bits(rng.standard_normal((rows, 4096)).astype(F32) * F32(0.02))
+    r = np.arange(rows)
+    w[r % 7 == 3] = to_bits(rng.standard_normal((int(np.sum(r % 7 == 3)), 4096)).astype(F32))
+    for sel, k in ((r % 11 == 5, 32), (r % 13 == 6, 33), (r % 17 == 8, 1)):
+        for i in np.nonzero(sel)[0]:
+            w[i] = to_bits(rng.uniform(0.01, 0.1, 4096).astype(F32))  # no natural escapes
+            w[i, rng.choice(4096, k, replace=False)] = 0
+    w[-1, 4095] = 0
+    got, p = packed_logits(env, x, w)
+    per_row = np.diff(np.append(p.offsets.reshape(rows, 16)[:, 0], p.exceptions.size))
+    assert {0, 1, 32, 33}.issubset(set(per_row.tolist())) and per_row.max() > 1000
+    want = oracle.head_bf16(x, w)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    again, _ = packed_logits(env, x, w)
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
