@@ -264,9 +264,9 @@ int w8a8_swiglu(void *stream, const void *gate, const void *up, size_t rows,
 /* Greedy selection (`select_token`, src/kernels.rs:2191-2231): the largest
  * value, lowest index on ties (-0 == +0); empty input or any non-finite
  * value gives 0xFFFFFFFF.  Multi-workgroup: needs a device workspace of at
- * least w8a8_select_workspace_bytes(n) bytes, zero-filled before its first
- * use (w8a8_malloc does that); every call leaves it zeroed again.  Calls
- * that share one workspace must not overlap. */
+ * least w8a8_select_workspace_bytes(n) bytes (one 8-byte key per
+ * workgroup).  It needs no initialisation: each call writes every key it
+ * reads.  Calls that share one workspace must not overlap. */
 size_t w8a8_select_workspace_bytes(size_t n);
 int w8a8_select_token(void *stream, const float *x, size_t n, uint32_t *token,
                       void *workspace, size_t workspace_bytes);

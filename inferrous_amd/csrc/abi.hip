@@ -8,6 +8,7 @@
 // no hipMemsetAsync (zeroing uses a fill kernel), hence graph-capturable.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <mutex>
@@ -579,7 +580,7 @@ int w8a8_linear_swiglu(void* stream, const int8_t* q, const float* asc, size_t m
 
 size_t w8a8_select_workspace_bytes(size_t n) {
   (void)n;
-  return kSelectSlots * kSelectStride * sizeof(uint64_t);
+  return kSelectBlocks * sizeof(uint64_t);
 }
 
 int w8a8_select_token(void* stream, const float* x, size_t n, uint32_t* token, void* workspace,
@@ -594,8 +595,7 @@ int w8a8_select_token(void* stream, const float* x, size_t n, uint32_t* token, v
 }
 
 size_t w8a8_linear_argmax_workspace_bytes(size_t n) {
-  (void)n;
-  return kSelectSlots * kSelectStride * sizeof(uint64_t);
+  return std::max<size_t>(1, argmax_keys_bound(n)) * sizeof(uint64_t);
 }
 
 int w8a8_linear_argmax(void* stream, const int8_t* q, const float* asc, const int8_t* w,

@@ -89,42 +89,64 @@ __device__ __forceinline__ int owner(const GemvArgs& a, uint32_t g) {
   return mi;
 }
 
-// Greedy selection across workgroups.  Every output row's key is folded
-// into one of kSelectSlots device words (slot = row mod kSelectSlots, one
-// 128-byte line apart) by the lane that computed it -- no barrier, no fence,
-// no spinning.  A slot only grows while the producer runs, so the lane first
-// reads it (device-coherent relaxed load) and issues the atomicMax only when
-// its key is larger: a stale read can cause a redundant atomic, never a
-// missed one, and on typical data almost every row skips the atomic.  A
-// one-wave finalize kernel, stream-ordered after the producer, exchanges the
-// slots back to zero and writes the token, leaving the workspace zeroed for
-// the next call (graph-replay safe without a memset).
-__device__ __forceinline__ void select_publish_lane(uint64_t key, uint32_t row, uint64_t* slots) {
-  uint64_t* sp = &slots[(row % kSelectSlots) * kSelectStride];
-  if (key > __hip_atomic_load(sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-    atomicMax((unsigned long long*)sp, (unsigned long long)key);
+// Greedy selection across workgroups, in two kernels and with no atomics on
+// device memory.  The producer's workgroup b writes the largest key of its
+// rows to keys[b]: its waves meet in LDS, and the wave that arrives last (an
+// LDS counter, zeroed behind a barrier at the workgroup's start) writes.  A
+// one-workgroup kernel, stream-ordered after the producer, reduces the keys
+// and writes the token.  Each call writes every key it reads, so the
+// workspace needs no initialisation and carries nothing between calls.
+struct SelectLds {
+  uint64_t key[kGemvWaves];
+  uint32_t arrived;
+};
+
+__device__ __forceinline__ void select_lds_init(SelectLds& s) {
+  if (threadIdx.x == 0) s.arrived = 0;
+  __syncthreads();
 }
 
-// Workgroup-level variant for the standalone selection kernel (few, large
-// workgroups): reduce in LDS first, then one atomic per workgroup.
-__device__ __forceinline__ void select_publish_block(uint64_t key, uint64_t* slots) {
-  __shared__ uint64_t wbest[kGemvWaves];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Every lane of every wave calls this once, with its key (0 for no row).
+__device__ __forceinline__ void select_publish_wave(uint64_t key, SelectLds& s, uint64_t* keys) {
   key = wave_max_u64(key);
-  if (lane == 0) wbest[wave] = key;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t b = wbest[0];
+  if ((threadIdx.x & 63) == 0) {
+    s.key[threadIdx.x >> 6] = key;
+    const uint32_t before =
+        __hip_atomic_fetch_add(&s.arrived, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (before == kGemvWaves - 1) {
+      uint64_t b = s.key[0];
 #pragma unroll
-    for (int i = 1; i < kGemvWaves; ++i) b = wbest[i] > b ? wbest[i] : b;
-    select_publish_lane(b, blockIdx.x, slots);
+      for (int i = 1; i < kGemvWaves; ++i) b = s.key[i] > b ? s.key[i] : b;
+      keys[blockIdx.x] = b;
+    }
   }
 }
 
-__global__ __launch_bounds__(64) void select_finalize(uint64_t* slots, uint32_t* token) {
-  uint64_t v = atomicExch((unsigned long long*)&slots[threadIdx.x * kSelectStride], 0ull);
-  v = wave_max_u64(v);
-  if (threadIdx.x == 0) *token = key_to_token(v);
+constexpr int kFinalizeThreads = 1024;
+constexpr int kFinalizeBatch = 48;  // keys per thread per round: 49,152 keys (a 196K vocabulary) in one
+
+// Latency-bound: each round issues all its loads before the first use (the
+// index is clamped rather than tested, so no load waits behind a branch).
+__global__ __launch_bounds__(kFinalizeThreads) void select_finalize(const uint64_t* __restrict__ keys,
+                                                                    uint32_t nkeys, uint32_t* token) {
+  __shared__ uint64_t wbest[kFinalizeThreads / 64];
+  uint64_t b = 0;
+  for (uint32_t base = 0; base < nkeys; base += kFinalizeThreads * kFinalizeBatch) {
+    uint64_t v[kFinalizeBatch];
+#pragma unroll
+    for (int u = 0; u < kFinalizeBatch; ++u)
+      v[u] = keys[min(base + u * kFinalizeThreads + threadIdx.x, nkeys - 1)];
+#pragma unroll
+    for (int u = 0; u < kFinalizeBatch; ++u) b = v[u] > b ? v[u] : b;
+  }
+  b = wave_max_u64(b);
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < kFinalizeThreads / 64; ++i) b = wbest[i] > b ? wbest[i] : b;
+    *token = key_to_token(b);
+  }
 }
 
 // M = 1, k = KC * 1024 known at compile time: activations held in registers.
@@ -137,15 +159,22 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_m1(GemvArgs a) {
   const uint32_t n = a.n[mi];
   const uint32_t row0 = live ? (g - a.gbegin[mi]) * R : 0;
   constexpr uint32_t K = KC * 1024;
+  __shared__ SelectLds sel;
+  if (EPI == EPI_ARGMAX) select_lds_init(sel);
 
   int acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0;
+  float wsc = 0.f;  // ws of this lane's output row (writer lanes)
   if (live) {
     const int8_t* __restrict__ W = a.w[mi];
     v4i x[KC];
 #pragma unroll
     for (int c = 0; c < KC; ++c) x[c] = load16(a.q + c * 1024 + lane * 16);
+    // The epilogue's operands are loaded ahead of the weight stream, so that
+    // their latency hides under it instead of extending the wave's life.
+    const uint32_t erow = min(row0 + (uint32_t)min(lane, R - 1), n - 1);
+    wsc = a.ws[mi][erow];
     v4i wv[R][KC];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -164,14 +193,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_m1(GemvArgs a) {
   const bool writer = live && lane < R && row < n;
   float value = 0.f;
   if (writer) {
-    value = dequant(total, a.asc[0], a.ws[mi][row]);
+    value = dequant(total, a.asc[0], wsc);
     if (a.out[mi]) store_out(a.out[mi], row, a.out_dtype, total, value);
     if (EPI == EPI_RESIDUAL) {
       const float comb = bf16_rne(a.residual[row] + value);
       store_out(a.combined, row, a.out_dtype, total, comb);
     }
   }
-  if (EPI == EPI_ARGMAX && writer) select_publish_lane(select_key(value, row), row, a.slots);
+  if (EPI == EPI_ARGMAX) select_publish_wave(writer ? select_key(value, row) : 0ull, sel, a.slots);
 }
 
 // Any m (blockIdx.y selects MT activation rows), any k % 16 == 0.
@@ -186,6 +215,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
   const uint32_t row0 = live ? (g - a.gbegin[mi]) * R : 0;
   const uint32_t m0 = blockIdx.y * MT;
   const uint32_t K = a.k;
+  __shared__ SelectLds sel;
+  if (EPI == EPI_ARGMAX) select_lds_init(sel);
 
   int acc[V];
 #pragma unroll
@@ -236,7 +267,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
       store_out(a.combined, o, a.out_dtype, total, comb);
     }
   }
-  if (EPI == EPI_ARGMAX && writer) select_publish_lane(select_key(value, row), row, a.slots);
+  if (EPI == EPI_ARGMAX) select_publish_wave(writer ? select_key(value, row) : 0ull, sel, a.slots);
 }
 
 // Producer side of the maxima protocol (publish_absmax, src/kernels.rs:133-147):
@@ -270,10 +301,15 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_swiglu(SwigluArgs a) {
   const bool live = c < a.n;
   constexpr uint32_t K = KC * 1024;
   int ag = 0, au = 0;
+  float wsg = 0.f, wsu = 0.f, asc = 0.f;
   if (live) {
     v4i x[KC], wg[KC], wu[KC];
 #pragma unroll
     for (int i = 0; i < KC; ++i) x[i] = load16(a.q + i * 1024 + lane * 16);
+    // epilogue operands ahead of the weight stream (latency hidden under it)
+    wsg = a.wsg[c];
+    wsu = a.wsu[c];
+    asc = a.asc[0];
     const int8_t* pg = a.wg + (size_t)c * K + lane * 16;
     const int8_t* pu = a.wu + (size_t)c * K + lane * 16;
 #pragma unroll
@@ -291,8 +327,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_swiglu(SwigluArgs a) {
   const int tu = wave_sum_uniform(au);
   uint32_t bits = 0;
   if (live && lane == 0) {
-    const float g = dequant(tg, a.asc[0], a.wsg[c]);
-    const float u = dequant(tu, a.asc[0], a.wsu[c]);
+    const float g = dequant(tg, asc, wsg);
+    const float u = dequant(tu, asc, wsu);
     const float v = silu_mul(g, u);
     store_out(a.gate, c, a.out_dtype, tg, g);
     store_out(a.up, c, a.out_dtype, tu, u);
@@ -328,14 +364,16 @@ __global__ __launch_bounds__(kGemvThreads) void swiglu_kernel(const void* gate, 
 
 // Standalone greedy selection over f32 values.
 __global__ __launch_bounds__(kGemvThreads) void select_kernel(const float* __restrict__ x, size_t n,
-                                                               uint64_t* slots) {
+                                                               uint64_t* keys) {
+  __shared__ SelectLds sel;
+  select_lds_init(sel);
   uint64_t best = 0;
   for (size_t i = (size_t)blockIdx.x * kGemvThreads + threadIdx.x; i < n;
        i += (size_t)gridDim.x * kGemvThreads) {
     const uint64_t k = select_key(x[i], (uint32_t)i);
     best = k > best ? k : best;
   }
-  select_publish_block(best, slots);
+  select_publish_wave(best, sel, keys);
 }
 
 __global__ void write_sentinel(uint32_t* token) {
@@ -354,22 +392,24 @@ static uint32_t count_groups(GemvArgs& a, const uint32_t* n, int count) {
   return g;
 }
 
+// Each launcher reports its grid's x extent in *blocks (the selection
+// finalize reads one key per workgroup).
 template <int R, int KC, int EPI>
-static hipError_t launch_m1(hipStream_t st, GemvArgs& a, const uint32_t* nn) {
+static hipError_t launch_m1(hipStream_t st, GemvArgs& a, const uint32_t* nn, uint32_t* blocks) {
   const uint32_t groups = count_groups<R>(a, nn, a.count);
+  *blocks = (groups + kGemvWaves - 1) / kGemvWaves;
   if (groups == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_m1<R, KC, EPI>), dim3((groups + kGemvWaves - 1) / kGemvWaves),
-                     dim3(kGemvThreads), 0, st, a);
+  hipLaunchKernelGGL((gemv_m1<R, KC, EPI>), dim3(*blocks), dim3(kGemvThreads), 0, st, a);
   return hipGetLastError();
 }
 
 template <int MT, int U, int EPI>
-static hipError_t launch_mt(hipStream_t st, GemvArgs& a, const uint32_t* nn) {
+static hipError_t launch_mt(hipStream_t st, GemvArgs& a, const uint32_t* nn, uint32_t* blocks) {
   const uint32_t groups = count_groups<4>(a, nn, a.count);
+  *blocks = (groups + kGemvWaves - 1) / kGemvWaves;
   if (groups == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_mt<4, MT, U, EPI>),
-                     dim3((groups + kGemvWaves - 1) / kGemvWaves, (a.m + MT - 1) / MT),
-                     dim3(kGemvThreads), 0, st, a);
+  hipLaunchKernelGGL((gemv_mt<4, MT, U, EPI>), dim3(*blocks, (a.m + MT - 1) / MT), dim3(kGemvThreads), 0,
+                     st, a);
   return hipGetLastError();
 }
 
@@ -377,7 +417,7 @@ static hipError_t launch_mt(hipStream_t st, GemvArgs& a, const uint32_t* nn) {
 // (one or two 4 KiB rows) and exit stream HBM better than longer batches or
 // grid-stride sweeps; two rows per wave helps only the small matrices.
 template <int EPI>
-static hipError_t dispatch(hipStream_t st, GemvArgs& a) {
+static hipError_t dispatch(hipStream_t st, GemvArgs& a, uint32_t* blocks) {
   uint32_t nn[kMaxGroup];
   uint64_t total = 0;
   for (int i = 0; i < a.count; ++i) {
@@ -385,17 +425,18 @@ static hipError_t dispatch(hipStream_t st, GemvArgs& a) {
     total += a.n[i];
   }
   if (a.m == 1 && a.k == 4096)
-    return total <= 8192 ? launch_m1<2, 4, EPI>(st, a, nn) : launch_m1<1, 4, EPI>(st, a, nn);
-  if (a.m == 1 && a.k == 12288) return launch_m1<1, 12, EPI>(st, a, nn);
-  if (a.m == 1 || EPI == EPI_ARGMAX) return launch_mt<1, 4, EPI>(st, a, nn);
-  if (a.m <= 2) return launch_mt<2, 4, EPI>(st, a, nn);
-  if (a.m <= 4) return launch_mt<4, 2, EPI>(st, a, nn);
-  return launch_mt<8, 2, EPI>(st, a, nn);
+    return total <= 8192 ? launch_m1<2, 4, EPI>(st, a, nn, blocks) : launch_m1<1, 4, EPI>(st, a, nn, blocks);
+  if (a.m == 1 && a.k == 12288) return launch_m1<1, 12, EPI>(st, a, nn, blocks);
+  if (a.m == 1 || EPI == EPI_ARGMAX) return launch_mt<1, 4, EPI>(st, a, nn, blocks);
+  if (a.m <= 2) return launch_mt<2, 4, EPI>(st, a, nn, blocks);
+  if (a.m <= 4) return launch_mt<4, 2, EPI>(st, a, nn, blocks);
+  return launch_mt<8, 2, EPI>(st, a, nn, blocks);
 }
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a) {
-  if (a.residual) return dispatch<EPI_RESIDUAL>(st, a);
-  return dispatch<EPI_PLAIN>(st, a);
+  uint32_t blocks = 0;
+  if (a.residual) return dispatch<EPI_RESIDUAL>(st, a, &blocks);
+  return dispatch<EPI_PLAIN>(st, a, &blocks);
 }
 
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
@@ -403,10 +444,16 @@ hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
     hipLaunchKernelGGL(write_sentinel, dim3(1), dim3(64), 0, st, a.token);
     return hipGetLastError();
   }
-  hipError_t e = dispatch<EPI_ARGMAX>(st, a);
+  uint32_t blocks = 0;
+  hipError_t e = dispatch<EPI_ARGMAX>(st, a, &blocks);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kSelectSlots), 0, st, a.slots, a.token);
+  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kFinalizeThreads), 0, st, a.slots, blocks, a.token);
   return hipGetLastError();
+}
+
+size_t argmax_keys_bound(size_t n) {
+  // every route puts at least one row per wave and kGemvWaves waves per workgroup
+  return (n + kGemvWaves - 1) / kGemvWaves;
 }
 
 hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {
@@ -438,17 +485,17 @@ hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_
   return hipSuccess;
 }
 
-hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* slots, uint32_t* token) {
+hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* keys, uint32_t* token) {
   if (n == 0) {
     hipLaunchKernelGGL(write_sentinel, dim3(1), dim3(64), 0, st, token);
     return hipGetLastError();
   }
   const uint64_t b = (n + kGemvThreads * 16 - 1) / (kGemvThreads * 16);
-  const unsigned blocks = (unsigned)(b > 1024 ? 1024 : b);
-  hipLaunchKernelGGL(select_kernel, dim3(blocks), dim3(kGemvThreads), 0, st, x, n, slots);
+  const unsigned blocks = (unsigned)(b > kSelectBlocks ? kSelectBlocks : b);
+  hipLaunchKernelGGL(select_kernel, dim3(blocks), dim3(kGemvThreads), 0, st, x, n, keys);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kSelectSlots), 0, st, slots, token);
+  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kFinalizeThreads), 0, st, keys, blocks, token);
   return hipGetLastError();
 }
 

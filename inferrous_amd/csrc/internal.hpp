@@ -10,8 +10,7 @@
 namespace w8a8 {
 
 constexpr int kMaxGroup = 4;
-constexpr int kSelectSlots = 64;   // selection workspace: 64 u64 slots, zero when idle,
-constexpr int kSelectStride = 16;  // one 128-byte line apart (stride in u64 units)
+constexpr int kSelectBlocks = 1024;  // stand-alone selection: at most this many workgroups (one u64 key each)
 
 // One GEMV launch: up to kMaxGroup sibling projections sharing q/asc.
 struct GemvArgs {
@@ -27,7 +26,7 @@ struct GemvArgs {
   int out_dtype;
   const float* residual;  // EPI residual (count == 1)
   void* combined;
-  uint64_t* slots;  // fused selection (count == 1, m == 1)
+  uint64_t* slots;  // fused selection (count == 1, m == 1): one u64 key per workgroup
   uint32_t* token;
 };
 
@@ -85,7 +84,9 @@ hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a);  // m == 1, k in {4096, 12288}
 hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_t rows,
                          uint32_t width, void* act, int dtype, uint32_t* maxima);
-hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* slots, uint32_t* token);
+hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* keys, uint32_t* token);
+// u64 keys the fused selection of an n-row lm_head writes (an upper bound)
+size_t argmax_keys_bound(size_t n);
 
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a);
 
