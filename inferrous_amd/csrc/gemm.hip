@@ -264,6 +264,78 @@ __device__ __forceinline__ void store_ep(const GemmArgs& a, uint32_t r, uint32_t
   }
 }
 
+// Epilogue of a wave's FM x FN grid of 32x32 accumulator blocks whose top
+// left corner is (row0, col0).  Lane l, value v of block (i, j) is row
+// row0 + 32i + 8(v / 4) + 4(l / 32) + v % 4, column col0 + 32j + l % 32.
+// Every operand the epilogue reads (row scales, column scales, residuals)
+// is loaded first, at clamped, always valid addresses, and every store comes
+// after the last use of a load: stores count in the same in-order counter
+// as loads, so a load issued after a store would wait for the store too.
+template <int EP, int FM, int FN>
+__device__ __forceinline__ void store_blocks(const GemmArgs& a, const v16i (&acc)[FM][FN], uint32_t row0,
+                                             uint32_t col0, int lane) {
+  constexpr bool RES = EP == EP_F32_RES || EP == EP_BF16_RES;
+  uint32_t rows[FM][16];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) rows[i][v] = row0 + 32 * i + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+  if (EP == EP_I32) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const uint32_t c = col0 + 32 * j + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (rows[i][v] < a.m && c < a.n)
+            reinterpret_cast<int32_t*>(a.out)[(size_t)rows[i][v] * a.n + c] = acc[i][j][v];
+    }
+    return;
+  }
+  float asc[FM][16], wsc[FN];
+  float res[RES ? FM : 1][RES ? FN : 1][16];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) asc[i][v] = a.asc[min(rows[i][v], a.m - 1)];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const uint32_t cc = min(col0 + 32 * j + (lane & 31), a.n - 1);
+    wsc[j] = a.ws[cc];
+    if (RES)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) res[i][j][v] = a.residual[(size_t)min(rows[i][v], a.m - 1) * a.n + cc];
+  }
+  // one wait for every load above, taken unconditionally: a wait first met
+  // inside a guarded store would be repeated in each guarded store after it
+  wait_vmcnt<0>();
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const uint32_t c = col0 + 32 * j + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const uint32_t r = rows[i][v];
+        const float val = dequant(acc[i][j][v], asc[i][v], wsc[j]);
+        if (r >= a.m || c >= a.n) continue;
+        const size_t o = (size_t)r * a.n + c;
+        if (EP == EP_F32 || EP == EP_F32_RES) {
+          if (a.out) reinterpret_cast<float*>(a.out)[o] = val;
+          if (RES) reinterpret_cast<float*>(a.combined)[o] = bf16_rne(res[RES ? i : 0][RES ? j : 0][v] + val);
+        } else {
+          if (a.out) reinterpret_cast<uint16_t*>(a.out)[o] = (uint16_t)(__float_as_uint(val) >> 16);
+          if (RES)
+            reinterpret_cast<uint16_t*>(a.combined)[o] =
+                (uint16_t)(__float_as_uint(bf16_rne(res[RES ? i : 0][RES ? j : 0][v] + val)) >> 16);
+        }
+      }
+  }
+}
+
 // Prefill GEMM.  Workgroup = 8 waves (two per SIMD: while one wave waits on
 // LDS the other keeps the matrix core busy), output tile BM x BN, wave tile
 // WM x WN built from 32x32 MFMA blocks.  K advances in 128-byte stages, so
@@ -424,19 +496,7 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   mm(a0, b0);
   mm(a1, b1);
 
-  // 32x32 result layout: lane l, value v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const uint32_t c = n0 + wn0 + j * 32 + (lane & 31);
-    const float wsc = (EP != EP_I32 && c < a.n) ? a.ws[c] : 0.f;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const uint32_t r = m0 + wm0 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (r < a.m && c < a.n) store_ep<EP>(a, r, c, acc[i][j][v], wsc);
-      }
-  }
+  store_blocks<EP, FM, FN>(a, acc, m0 + wm0, n0 + wn0, lane);
 }
 
 template <int BM, int BN, int WM, int WN, int SA, int SB>
@@ -453,6 +513,191 @@ static void launch_dma(hipStream_t st, const GemmArgs& a) {
     hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16_RES>), grid, block, 0, st, a, tm, tn, 1u);
   else
     hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16>), grid, block, 0, st, a, tm, tn, 1u);
+}
+
+// Cache policy of a load streamed once (the weights of a single M tile): the
+// non-temporal bit, so the lines do not displace the activations that every
+// workgroup re-reads from L2.
+constexpr int kCpolNT = 2;
+
+// s_waitcnt vmcnt(n) for a wave-uniform n known only at run time (n <= 20).
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+  switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 9: wait_vmcnt<9>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 11: wait_vmcnt<11>(); break;
+    case 12: wait_vmcnt<12>(); break;
+    case 13: wait_vmcnt<13>(); break;
+    case 14: wait_vmcnt<14>(); break;
+    case 15: wait_vmcnt<15>(); break;
+    case 16: wait_vmcnt<16>(); break;
+    case 17: wait_vmcnt<17>(); break;
+    case 18: wait_vmcnt<18>(); break;
+    case 19: wait_vmcnt<19>(); break;
+    default: wait_vmcnt<20>(); break;
+  }
+}
+
+// Prefill GEMM for 128 < M <= MA (gemm_tall, MA = 160 or 256).  One M tile
+// of MA rows holds every activation row, so each weight tile is read from
+// HBM once, and no DMA or MFMA goes to a second M tile holding a few rows.
+// The eight waves are stacked along M (wave w: rows 32w .. 32w + 31, all BN
+// columns); a wave whose rows all lie past M only moves data.
+//
+// Rings as in gemm_dma: activations (SA slots of MA rows; the lines are
+// shared by every workgroup and come from L2 or MALL) and weights (SB slots;
+// the lines come from HBM and are read once, non-temporal).  With few MFMAs
+// per stage the stage is short, so both rings look several stages ahead.  A
+// stage's DMA instructions (8 rows x 128 bytes each) are dealt to the waves
+// round-robin, separately for the ceil(M / 8) activation row groups -- rows
+// past the last group are never loaded -- and the BN / 8 weight row groups,
+// so a wave issues na activation and nb weight instructions per stage and
+// counts its waits with its own na, nb.  During stage kt it issues
+// A(kt + SA - 1), then B(kt + SB - 1).
+// Split-K as in gemm_dma: workgroup (tile, split) writes i32 slab `split`.
+template <int BN, int SA, int SB, int MA, int EP>
+__global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, uint32_t splits) {
+  constexpr int FN = BN / 32;
+  constexpr int ASL = MA * 128, BSL = BN * 128;
+  constexpr uint32_t NB = BN / 8;
+  constexpr int kMaxA = (MA / 8 + 7) / 8, kMaxB = (NB + 7) / 8;
+  static_assert(BN % 32 == 0 && BN <= 128 && MA % 32 == 0 && MA <= 256, "tile");
+  static_assert(SA >= 2 && SB > SA && SA * ASL + SB * BSL <= 160 * 1024, "LDS");
+  static_assert(kMaxB + (SA - 2) * (kMaxA + kMaxB) <= 20 && (SA - 2) * kMaxA + (SB - 2) * kMaxB <= 20,
+                "wait range");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[SA * ASL + SB * BSL];
+  int8_t* const ldsA = lds;
+  int8_t* const ldsB = lds + SA * ASL;
+
+  const uint32_t G = tiles_n * splits;
+  uint32_t Lt = blockIdx.x;
+  if (G % 8 == 0) Lt = (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8;
+  const uint32_t split = Lt / tiles_n;
+  const uint32_t n0 = (Lt % tiles_n) * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const uint32_t K = a.k, KT = K / 128 / splits;
+  const size_t kbase = (size_t)split * KT * 128;
+  if (EP == EP_I32) a.out = reinterpret_cast<int32_t*>(a.out) + (size_t)split * a.m * a.n;
+
+  // This wave's DMA instructions: activation row groups w, w + 8, ... below
+  // ceil(M / 8), weight row groups w, w + 8, ... below BN / 8.  Lane l fills
+  // LDS chunk l % 8 of row l / 8 with global chunk (l % 8) ^ key(row).
+  const uint32_t NA = (a.m + 7) / 8;
+  const int na = (int)((NA + 7 - (uint32_t)wave) / 8);
+  const int nb = (int)((NB + 7 - (uint32_t)wave) / 8);
+  const int8_t* srcA[kMaxA];
+  const int8_t* srcB[kMaxB];
+#pragma unroll
+  for (int j = 0; j < kMaxA; ++j) {
+    const uint32_t row = 8 * (wave + 8 * j) + (lane >> 3);
+    srcA[j] = a.q + (size_t)min(row, a.m - 1) * K + kbase + ((lane & 7) ^ ((row >> 1) & 7)) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxB; ++j) {
+    const uint32_t br = 8 * (wave + 8 * j) + (lane >> 3);  // row within the weight tile
+    srcB[j] = a.w + (size_t)min(n0 + br, a.n - 1) * K + kbase + ((lane & 7) ^ ((br >> 1) & 7)) * 16;
+  }
+  auto issueA = [&](uint32_t kt) {
+#pragma unroll
+    for (int j = 0; j < kMaxA; ++j)
+      if (j < na)
+        __builtin_amdgcn_global_load_lds((const void*)(srcA[j] + (size_t)kt * 128),
+                                         W8A8_LDS_PTR(ldsA + (kt % SA) * ASL + 1024 * (wave + 8 * j) + lane * 16),
+                                         16, 0, 0);
+  };
+  auto issueB = [&](uint32_t kt) {
+#pragma unroll
+    for (int j = 0; j < kMaxB; ++j)
+      if (j < nb)
+        __builtin_amdgcn_global_load_lds((const void*)(srcB[j] + (size_t)kt * 128),
+                                         W8A8_LDS_PTR(ldsB + (kt % SB) * BSL + 1024 * (wave + 8 * j) + lane * 16),
+                                         16, 0, kCpolNT);
+  };
+  auto batch = [&](uint32_t kt) {
+    if (kt + SA - 1 < KT) issueA(kt + SA - 1);
+    if (kt + SB - 1 < KT) issueB(kt + SB - 1);
+  };
+  // end of stage kt: A(kt + 1) and B(kt + 1) landed; in flight may remain the
+  // B half of A(kt + 1)'s batch and the SA - 2 whole batches after it
+  auto wait_next = [&](uint32_t kt) {
+    if (kt + SB - 1 < KT) wait_vmcnt_dyn(nb + (SA - 2) * (na + nb));
+    else wait_vmcnt<0>();
+  };
+
+  const int fr = lane & 31, fh = lane >> 5;
+  int off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) off[i] = fr * 128 + (((2 * i + fh) ^ ((fr >> 1) & 7)) * 16);
+  v16i acc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) acc[j] = v16i{};
+  auto rd = [&](uint32_t kt, int i, v4i& af, v4i (&bf)[FN]) {
+    af = *(const v4i*)(ldsA + (kt % SA) * ASL + (32 * wave) * 128 + off[i]);
+    const int8_t* bb = ldsB + (kt % SB) * BSL;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(bb + (32 * j) * 128 + off[i]);
+  };
+  auto mm = [&](const v4i& af, const v4i (&bf)[FN]) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[j] = mfma32(af, bf[j], acc[j]);
+  };
+
+  // Prologue: stages 0 .. SB - 2 (activations up to SA - 2), stage by stage;
+  // then wait for A(0) and B(0).
+  for (int s = 0; s < SB - 1; ++s) {
+    if (s >= (int)KT) break;
+    if (s < SA - 1) issueA(s);
+    issueB(s);
+  }
+  if (KT >= (uint32_t)SB - 1) wait_vmcnt_dyn((SA - 2) * na + (SB - 2) * nb);
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  if (32u * wave < a.m) {
+    v4i a0, b0[FN], a1, b1[FN];
+    batch(0);
+    rd(0, 0, a0, b0);
+    for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+      rd(kt, 1, a1, b1);
+      mm(a0, b0);
+      rd(kt, 2, a0, b0);
+      mm(a1, b1);
+      rd(kt, 3, a1, b1);
+      mm(a0, b0);
+      wait_next(kt);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of stage kt returned
+      __builtin_amdgcn_s_barrier();
+      batch(kt + 1);
+      rd(kt + 1, 0, a0, b0);
+      mm(a1, b1);
+    }
+    rd(KT - 1, 1, a1, b1);
+    mm(a0, b0);
+    rd(KT - 1, 2, a0, b0);
+    mm(a1, b1);
+    rd(KT - 1, 3, a1, b1);
+    mm(a0, b0);
+    mm(a1, b1);
+    const v16i (&blocks)[1][FN] = *reinterpret_cast<const v16i(*)[1][FN]>(&acc);
+    store_blocks<EP, 1, FN>(a, blocks, 32 * wave, n0, lane);
+  } else {
+    // rows past M: this wave only moves its share of the data
+    batch(0);
+    for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+      wait_next(kt);
+      __builtin_amdgcn_s_barrier();
+      batch(kt + 1);
+    }
+  }
 }
 
 // Split-K epilogue: out[r][c] = epilogue(sum over slabs of partials[s][r][c]).
@@ -496,11 +741,47 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, int& tile, uint32_t& 
   return kt % splits == 0 && kt / splits >= 4;
 }
 
+// gemm_tall plan for 128 < m <= 256 (measured on MI355X at M = 129 on the
+// Qwen3-8B projection shapes): 96-column tiles when they alone give about
+// one tile per CU; otherwise split K four ways (two when K is short), with
+// 96- or 64-column tiles, to reach about one workgroup per CU.  Returns
+// false when neither applies (the gemm_dma routes then run).
+static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits) {
+  if (m <= 128 || m > 256 || k % 128 != 0) return false;
+  const uint32_t kt = k / 128, t96 = (n + 95) / 96;
+  if (t96 >= 224) {
+    bn = 96;
+    splits = 1;
+    return true;
+  }
+  if (n % 4 != 0) return false;  // the split-K epilogue works on column quads
+  splits = (kt % 4 == 0 && kt / 4 >= 4) ? 4 : (kt % 2 == 0 && kt / 2 >= 4) ? 2 : 1;
+  if (splits == 1) return false;
+  bn = t96 * splits >= 224 ? 96 : 64;
+  return true;
+}
+
 size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
   int tile;
   uint32_t splits;
+  if (tall_plan(m, n, k, tile, splits)) return splits > 1 ? (size_t)splits * m * n * sizeof(int32_t) : 0;
   if (!split_plan(m, n, k, tile, splits)) return 0;
   return (size_t)splits * m * n * sizeof(int32_t);
+}
+
+static hipError_t launch_splitk_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits) {
+  const dim3 grid((a.n / 4 + 255) / 256, std::min<uint32_t>(a.m, 65535));
+  if (a.out_dtype == W8A8_OUT_I32)
+    hipLaunchKernelGGL(splitk_epilogue<EP_I32>, grid, dim3(256), 0, st, a, a.partials, splits);
+  else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
+    hipLaunchKernelGGL(splitk_epilogue<EP_F32_RES>, grid, dim3(256), 0, st, a, a.partials, splits);
+  else if (a.out_dtype == W8A8_OUT_F32)
+    hipLaunchKernelGGL(splitk_epilogue<EP_F32>, grid, dim3(256), 0, st, a, a.partials, splits);
+  else if (a.residual)
+    hipLaunchKernelGGL(splitk_epilogue<EP_BF16_RES>, grid, dim3(256), 0, st, a, a.partials, splits);
+  else
+    hipLaunchKernelGGL(splitk_epilogue<EP_BF16>, grid, dim3(256), 0, st, a, a.partials, splits);
+  return hipGetLastError();
 }
 
 template <int BM, int BN, int WM, int WN, int SA, int SB>
@@ -513,17 +794,32 @@ static hipError_t launch_split(hipStream_t st, const GemmArgs& a, uint32_t split
                      tm, tn, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const dim3 grid((a.n / 4 + 255) / 256, std::min<uint32_t>(a.m, 65535));
+  return launch_splitk_epilogue(st, a, splits);
+}
+
+template <int BN, int SA, int SB, int MA>
+static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits) {
+  const uint32_t tn = (a.n + BN - 1) / BN;
+  const dim3 grid(tn * splits), block(512);
+  if (splits > 1) {
+    GemmArgs p = a;
+    p.out = a.partials;
+    p.out_dtype = W8A8_OUT_I32;
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32>), grid, block, 0, st, p, tn, splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_splitk_epilogue(st, a, splits);
+  }
   if (a.out_dtype == W8A8_OUT_I32)
-    hipLaunchKernelGGL(splitk_epilogue<EP_I32>, grid, dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32>), grid, block, 0, st, a, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    hipLaunchKernelGGL(splitk_epilogue<EP_F32_RES>, grid, dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32_RES>), grid, block, 0, st, a, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32)
-    hipLaunchKernelGGL(splitk_epilogue<EP_F32>, grid, dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32>), grid, block, 0, st, a, tn, 1u);
   else if (a.residual)
-    hipLaunchKernelGGL(splitk_epilogue<EP_BF16_RES>, grid, dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16_RES>), grid, block, 0, st, a, tn, 1u);
   else
-    hipLaunchKernelGGL(splitk_epilogue<EP_BF16>, grid, dim3(256), 0, st, a, a.partials, splits);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16>), grid, block, 0, st, a, tn, 1u);
   return hipGetLastError();
 }
 
@@ -546,6 +842,13 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   } else if (a.k % 128 == 0) {
     int tile;
     uint32_t splits;
+    if (tall_plan(a.m, a.n, a.k, tile, splits) &&
+        (splits == 1 || (a.partials && a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))))
+    {
+      if (a.m <= 160)
+        return tile == 96 ? launch_tall<96, 4, 6, 160>(st, a, splits) : launch_tall<64, 4, 9, 160>(st, a, splits);
+      return tile == 96 ? launch_tall<96, 2, 8, 256>(st, a, splits) : launch_tall<64, 2, 12, 256>(st, a, splits);
+    }
     if (a.partials && split_plan(a.m, a.n, a.k, tile, splits) &&
         a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))
       return tile == 0 ? launch_split<128, 128, 32, 64, 4, 4>(st, a, splits)

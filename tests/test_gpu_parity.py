@@ -369,7 +369,7 @@ def test_errors_raise_not_fall_back(env):
 
 
 # ------------------------------------------------------------------ split-K workspace
-@pytest.mark.parametrize("m,n,k", [(129, 4096, 12288), (512, 4096, 12288), (129, 4096, 4096),
+@pytest.mark.parametrize("m,n,k", [(129, 4096, 12288), (512, 4096, 12288), (129, 4096, 4096), (129, 6144, 4096),
                                    (100, 96, 12288), (255, 1024, 4096)])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
@@ -404,6 +404,49 @@ def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
         assert np.array_equal(o.view(np.uint8), outs[0][0].view(np.uint8))
         if res:
             assert np.array_equal(c, outs[0][1])
+    acc, of, ob = oracle.linear(q, asc, w, ws, k, threads=8)
+    got = outs[0][0]
+    if dtype == np.int32:
+        assert np.array_equal(got, acc)
+    elif dtype == np.uint16:
+        assert np.array_equal(got, ob)
+        want = (bits(oracle.residual(resid, of)) >> 16).astype(np.uint16)
+        assert np.array_equal(outs[0][1], want)
+    else:
+        assert np.array_equal(bits(got), bits(of))
+
+
+@pytest.mark.parametrize("m", [129, 193, 256])
+@pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
+def test_linear_one_m_tile_wide_n(env, m, dtype, res):
+    """128 < M <= 256 on a wide N (the gate_up regime): one 256-row M tile,
+    waves past M idle, activation rows past M never loaded, a ragged last
+    column tile; bit-exact against the oracle with and without a workspace."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    n, k = 21601, 1024
+    print(f"one-M-tile m={m} n={n} k={k} {np.dtype(dtype).name} res={res}", flush=True)
+    lib = _lib.lib()
+    rng = np.random.default_rng(m * 7 + 3)
+    q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    q[-1] = 127
+    w[-1] = -127
+    asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    resid = oracle.bf16_rne(rng.standard_normal(m * n).astype(F32))
+    dq, da, dw, dws, dres = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws), dev(s, resid)
+    dt = {np.float32: _lib.OUT_F32, np.uint16: _lib.OUT_BF16, np.int32: _lib.OUT_I32}[dtype]
+    work = DeviceBuffer.zeroed(s, 4 * m * n * 4, np.uint8)
+    outs = []
+    for wp, wb in ((None, 0), (work.ptr, 4 * m * n * 4)):
+        out = DeviceBuffer.zeroed(s, m * n, dtype)
+        comb = DeviceBuffer.zeroed(s, m * n, dtype) if res else None
+        _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k,
+                                      dres.ptr if res else None, out.ptr,
+                                      comb.ptr if res else None, dt, _lib.PATH_AUTO, wp, wb))
+        outs.append((out.to_host_vec(s), comb.to_host_vec(s) if res else None))
+    assert np.array_equal(outs[1][0].view(np.uint8), outs[0][0].view(np.uint8))
     acc, of, ob = oracle.linear(q, asc, w, ws, k, threads=8)
     got = outs[0][0]
     if dtype == np.int32:
