@@ -19,7 +19,6 @@
 namespace w8a8 {
 
 constexpr int kQThreads = 256;
-constexpr int kQMaxVec = 16;  // f32: 16 x float4 per thread = 16384 wide
 
 __device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
   m = wave_max_u32(m);
@@ -29,7 +28,12 @@ __device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
   return max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
-// f32 rows, width % 4 == 0, 16-byte aligned rows.
+// f32 rows, width % 4 == 0, 16-byte aligned rows.  NV = float4 per thread
+// held in registers (NV * 256 * 4 >= width), or 0: the row is streamed
+// twice (the second pass hits L2).  The NV loads are issued unconditionally
+// (indices clamped to the row) so they are all in flight at once; a load
+// guarded by its own branch would be waited for before the next is issued.
+template <int NV>
 __global__ __launch_bounds__(kQThreads) void quantize_f32_vec(
     const float* __restrict__ x, uint32_t width, int8_t* __restrict__ q,
     float* __restrict__ scales, uint32_t* __restrict__ maxima_reset) {
@@ -39,26 +43,19 @@ __global__ __launch_bounds__(kQThreads) void quantize_f32_vec(
   const v4f* row = reinterpret_cast<const v4f*>(x + r * width);
   uint32_t* qrow = reinterpret_cast<uint32_t*>(q + r * width);
   const uint32_t t = threadIdx.x;
-  const bool in_regs = nvec <= kQThreads * kQMaxVec;
-
-  v4f v[kQMaxVec];
+  auto absmax4 = [](v4f a) {
+    return max(max(abs_bits_no_nan(a.x), abs_bits_no_nan(a.y)), max(abs_bits_no_nan(a.z), abs_bits_no_nan(a.w)));
+  };
+  v4f v[NV > 0 ? NV : 1];
   uint32_t m = kFloorBits;
-  if (in_regs) {
+  if (NV > 0) {
 #pragma unroll
-    for (int i = 0; i < kQMaxVec; ++i) {
-      const uint32_t j = t + i * kQThreads;
-      if (j < nvec) {
-        v[i] = row[j];
-        m = max(m, max(max(abs_bits_no_nan(v[i].x), abs_bits_no_nan(v[i].y)),
-                       max(abs_bits_no_nan(v[i].z), abs_bits_no_nan(v[i].w))));
-      }
-    }
+    for (int i = 0; i < NV; ++i) v[i] = row[min(t + i * kQThreads, nvec - 1)];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (t + i * kQThreads < nvec) m = max(m, absmax4(v[i]));
   } else {
-    for (uint32_t j = t; j < nvec; j += kQThreads) {
-      v4f a = row[j];
-      m = max(m, max(max(abs_bits_no_nan(a.x), abs_bits_no_nan(a.y)),
-                     max(abs_bits_no_nan(a.z), abs_bits_no_nan(a.w))));
-    }
+    for (uint32_t j = t; j < nvec; j += kQThreads) m = max(m, absmax4(row[j]));
   }
   m = block_max_256(m, red);
   const float s = __uint_as_float(m) / 127.0f;
@@ -66,9 +63,9 @@ __global__ __launch_bounds__(kQThreads) void quantize_f32_vec(
     scales[r] = s;
     if (maxima_reset) maxima_reset[r] = kFloorBits;
   }
-  if (in_regs) {
+  if (NV > 0) {
 #pragma unroll
-    for (int i = 0; i < kQMaxVec; ++i) {
+    for (int i = 0; i < NV; ++i) {
       const uint32_t j = t + i * kQThreads;
       if (j < nvec) qrow[j] = pack4(v[i].x, v[i].y, v[i].z, v[i].w, s);
     }
@@ -82,20 +79,20 @@ __global__ __launch_bounds__(kQThreads) void quantize_f32_vec(
 
 __device__ __forceinline__ float widen(uint32_t h) { return __uint_as_float(h << 16); }
 
-// BF16 rows, width % 8 == 0, 16-byte aligned rows: 8 values per 16 bytes.
+// BF16 rows, width % 8 == 0, 16-byte aligned rows: 8 values per 16 bytes;
+// NV as above (16-byte vectors per thread).
+template <int NV>
 __global__ __launch_bounds__(kQThreads) void quantize_bf16_vec(
     const uint16_t* __restrict__ x, uint32_t width, int8_t* __restrict__ q,
     float* __restrict__ scales, uint32_t* __restrict__ maxima_reset) {
   __shared__ uint32_t red[4];
-  constexpr int kMax = kQMaxVec / 2;
   const size_t r = blockIdx.x;
   const uint32_t nvec = width >> 3;
   const v4i* row = reinterpret_cast<const v4i*>(x + r * width);
   v2i* qrow = reinterpret_cast<v2i*>(q + r * width);
   const uint32_t t = threadIdx.x;
-  const bool in_regs = nvec <= kQThreads * kMax;
 
-  v4i v[kMax];
+  v4i v[NV > 0 ? NV : 1];
   uint32_t m = kFloorBits;
   auto absmax8 = [](v4i a) {
     uint32_t mm = 0;
@@ -114,15 +111,12 @@ __global__ __launch_bounds__(kQThreads) void quantize_bf16_vec(
                      widen((uint32_t)a.w & 0xffffu), widen((uint32_t)a.w >> 16), s);
     return o;
   };
-  if (in_regs) {
+  if (NV > 0) {
 #pragma unroll
-    for (int i = 0; i < kMax; ++i) {
-      const uint32_t j = t + i * kQThreads;
-      if (j < nvec) {
-        v[i] = row[j];
-        m = max(m, absmax8(v[i]));
-      }
-    }
+    for (int i = 0; i < NV; ++i) v[i] = row[min(t + i * kQThreads, nvec - 1)];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (t + i * kQThreads < nvec) m = max(m, absmax8(v[i]));
   } else {
     for (uint32_t j = t; j < nvec; j += kQThreads) m = max(m, absmax8(row[j]));
   }
@@ -132,9 +126,9 @@ __global__ __launch_bounds__(kQThreads) void quantize_bf16_vec(
     scales[r] = s;
     if (maxima_reset) maxima_reset[r] = kFloorBits;
   }
-  if (in_regs) {
+  if (NV > 0) {
 #pragma unroll
-    for (int i = 0; i < kMax; ++i) {
+    for (int i = 0; i < NV; ++i) {
       const uint32_t j = t + i * kQThreads;
       if (j < nvec) qrow[j] = quant8(v[i], s);
     }
@@ -265,12 +259,18 @@ hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t wi
                            int8_t* q, float* scales, uint32_t* maxima_reset) {
   if (rows == 0 || width == 0) return hipSuccess;
   dim3 grid((unsigned)rows), block(kQThreads);
-  if (!bf16 && width % 4 == 0 && aligned16(x) && ((uintptr_t)q & 3u) == 0)
-    hipLaunchKernelGGL(quantize_f32_vec, grid, block, 0, st, (const float*)x, width, q, scales,
-                       maxima_reset);
-  else if (bf16 && width % 8 == 0 && aligned16(x) && ((uintptr_t)q & 7u) == 0)
-    hipLaunchKernelGGL(quantize_bf16_vec, grid, block, 0, st, (const uint16_t*)x, width, q, scales,
-                       maxima_reset);
+  if (!bf16 && width % 4 == 0 && aligned16(x) && ((uintptr_t)q & 3u) == 0) {
+    const uint32_t nv = (width / 4 + kQThreads - 1) / kQThreads;  // float4 per thread
+    auto k = nv <= 1 ? quantize_f32_vec<1> : nv <= 2 ? quantize_f32_vec<2> : nv <= 4 ? quantize_f32_vec<4>
+           : nv <= 8 ? quantize_f32_vec<8> : nv <= 12 ? quantize_f32_vec<12>
+           : nv <= 16 ? quantize_f32_vec<16> : quantize_f32_vec<0>;
+    hipLaunchKernelGGL(k, grid, block, 0, st, (const float*)x, width, q, scales, maxima_reset);
+  } else if (bf16 && width % 8 == 0 && aligned16(x) && ((uintptr_t)q & 7u) == 0) {
+    const uint32_t nv = (width / 8 + kQThreads - 1) / kQThreads;  // 16-byte vectors per thread
+    auto k = nv <= 1 ? quantize_bf16_vec<1> : nv <= 2 ? quantize_bf16_vec<2> : nv <= 4 ? quantize_bf16_vec<4>
+           : nv <= 6 ? quantize_bf16_vec<6> : nv <= 8 ? quantize_bf16_vec<8> : quantize_bf16_vec<0>;
+    hipLaunchKernelGGL(k, grid, block, 0, st, (const uint16_t*)x, width, q, scales, maxima_reset);
+  }
   else if (bf16)
     hipLaunchKernelGGL(quantize_scalar<true>, grid, block, 0, st, x, width, q, scales, maxima_reset);
   else
