@@ -246,24 +246,6 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the residual sum bf(residual + out).
 enum { EP_I32 = 0, EP_F32 = 1, EP_BF16 = 2, EP_F32_RES = 3, EP_BF16_RES = 4 };
 
-template <int EP>
-__device__ __forceinline__ void store_ep(const GemmArgs& a, uint32_t r, uint32_t c, int32_t acc, float wsc) {
-  const size_t o = (size_t)r * a.n + c;
-  if (EP == EP_I32) {
-    reinterpret_cast<int32_t*>(a.out)[o] = acc;
-    return;
-  }
-  const float v = dequant(acc, a.asc[r], wsc);
-  if (EP == EP_F32 || EP == EP_F32_RES) {
-    if (a.out) reinterpret_cast<float*>(a.out)[o] = v;
-    if (EP == EP_F32_RES) reinterpret_cast<float*>(a.combined)[o] = bf16_rne(a.residual[o] + v);
-  } else {
-    if (a.out) reinterpret_cast<uint16_t*>(a.out)[o] = (uint16_t)(__float_as_uint(v) >> 16);
-    if (EP == EP_BF16_RES)
-      reinterpret_cast<uint16_t*>(a.combined)[o] = (uint16_t)(__float_as_uint(bf16_rne(a.residual[o] + v)) >> 16);
-  }
-}
-
 // Epilogue of a wave's FM x FN grid of 32x32 accumulator blocks whose top
 // left corner is (row0, col0).  Lane l, value v of block (i, j) is row
 // row0 + 32i + 8(v / 4) + 4(l / 32) + v % 4, column col0 + 32j + l % 32.
@@ -700,6 +682,8 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
   }
 }
 
+constexpr uint32_t kMaxSplits = 4;  // split-K plans use 2 or 4 slabs
+
 // Split-K epilogue: out[r][c] = epilogue(sum over slabs of partials[s][r][c]).
 // The i32 sum is exact in any order.  blockIdx.y walks rows (the row scale is
 // one scalar load), each thread four consecutive columns (n % 4 == 0), so the
@@ -707,6 +691,7 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
 template <int EP>
 __global__ __launch_bounds__(256) void splitk_epilogue(GemmArgs a, const int32_t* __restrict__ partials,
                                                         uint32_t splits) {
+  constexpr bool RES = EP == EP_F32_RES || EP == EP_BF16_RES;
   const size_t mn = (size_t)a.m * a.n;
   const uint32_t c = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= a.n) return;
@@ -716,10 +701,39 @@ __global__ __launch_bounds__(256) void splitk_epilogue(GemmArgs a, const int32_t
     for (int j = 0; j < 4; ++j) wsc[j] = a.ws[c + j];
   for (uint32_t r = blockIdx.y; r < a.m; r += gridDim.y) {
     const size_t i = (size_t)r * a.n + c;
-    v4i acc = *reinterpret_cast<const v4i*>(partials + i);
-    for (uint32_t s = 1; s < splits; ++s) acc += *reinterpret_cast<const v4i*>(partials + s * mn + i);
+    // every operand of the row first -- up to kMaxSplits slabs (slab index
+    // clamped, surplus slabs masked), the row scale, the residuals -- so one
+    // load round trip covers them; the stores come last
+    v4i part[kMaxSplits];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) store_ep<EP>(a, r, c + j, acc[j], wsc[j]);
+    for (uint32_t s = 0; s < kMaxSplits; ++s)
+      part[s] = *reinterpret_cast<const v4i*>(partials + min(s, splits - 1) * mn + i);
+    const float asc = EP != EP_I32 ? a.asc[r] : 0.f;
+    float res[4] = {0.f, 0.f, 0.f, 0.f};
+    if (RES)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) res[j] = a.residual[i + j];
+    v4i acc = part[0];
+#pragma unroll
+    for (uint32_t s = 1; s < kMaxSplits; ++s)
+      if (s < splits) acc += part[s];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const size_t o = i + j;
+      if (EP == EP_I32) {
+        reinterpret_cast<int32_t*>(a.out)[o] = acc[j];
+        continue;
+      }
+      const float v = dequant(acc[j], asc, wsc[j]);
+      if (EP == EP_F32 || EP == EP_F32_RES) {
+        if (a.out) reinterpret_cast<float*>(a.out)[o] = v;
+        if (RES) reinterpret_cast<float*>(a.combined)[o] = bf16_rne(res[j] + v);
+      } else {
+        if (a.out) reinterpret_cast<uint16_t*>(a.out)[o] = (uint16_t)(__float_as_uint(v) >> 16);
+        if (RES)
+          reinterpret_cast<uint16_t*>(a.combined)[o] = (uint16_t)(__float_as_uint(bf16_rne(res[j] + v)) >> 16);
+      }
+    }
   }
 }
 
@@ -770,6 +784,7 @@ size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
 }
 
 static hipError_t launch_splitk_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits) {
+  if (splits < 1 || splits > kMaxSplits) return hipErrorInvalidValue;
   const dim3 grid((a.n / 4 + 255) / 256, std::min<uint32_t>(a.m, 65535));
   if (a.out_dtype == W8A8_OUT_I32)
     hipLaunchKernelGGL(splitk_epilogue<EP_I32>, grid, dim3(256), 0, st, a, a.partials, splits);

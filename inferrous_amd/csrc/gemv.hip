@@ -123,21 +123,22 @@ __device__ __forceinline__ void select_publish_wave(uint64_t key, SelectLds& s, 
 }
 
 constexpr int kFinalizeThreads = 1024;
-constexpr int kFinalizeBatch = 48;  // keys per thread per round: 49,152 keys (a 196K vocabulary) in one
 
 // Latency-bound: each round issues all its loads before the first use (the
 // index is clamped rather than tested, so no load waits behind a branch).
+// B keys per thread per round, chosen by the launcher from the key count so
+// that a small key set is not re-read B times over.
+template <int B>
 __global__ __launch_bounds__(kFinalizeThreads) void select_finalize(const uint64_t* __restrict__ keys,
                                                                     uint32_t nkeys, uint32_t* token) {
   __shared__ uint64_t wbest[kFinalizeThreads / 64];
   uint64_t b = 0;
-  for (uint32_t base = 0; base < nkeys; base += kFinalizeThreads * kFinalizeBatch) {
-    uint64_t v[kFinalizeBatch];
+  for (uint32_t base = 0; base < nkeys; base += kFinalizeThreads * B) {
+    uint64_t v[B];
 #pragma unroll
-    for (int u = 0; u < kFinalizeBatch; ++u)
-      v[u] = keys[min(base + u * kFinalizeThreads + threadIdx.x, nkeys - 1)];
+    for (int u = 0; u < B; ++u) v[u] = keys[min(base + u * kFinalizeThreads + threadIdx.x, nkeys - 1)];
 #pragma unroll
-    for (int u = 0; u < kFinalizeBatch; ++u) b = v[u] > b ? v[u] : b;
+    for (int u = 0; u < B; ++u) b = v[u] > b ? v[u] : b;
   }
   b = wave_max_u64(b);
   if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
@@ -362,16 +363,27 @@ __global__ __launch_bounds__(kGemvThreads) void swiglu_kernel(const void* gate, 
   if (maxima) publish_absmax_block(bits, maxima + r);
 }
 
-// Standalone greedy selection over f32 values.
+// Standalone greedy selection over f32 values.  Each thread takes
+// kSelectPer values per pass, all loaded before any is compared (indices
+// clamped), so a pass costs one load round trip.
+constexpr int kSelectPer = 16;
+
 __global__ __launch_bounds__(kGemvThreads) void select_kernel(const float* __restrict__ x, size_t n,
                                                                uint64_t* keys) {
   __shared__ SelectLds sel;
   select_lds_init(sel);
   uint64_t best = 0;
-  for (size_t i = (size_t)blockIdx.x * kGemvThreads + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * kGemvThreads) {
-    const uint64_t k = select_key(x[i], (uint32_t)i);
-    best = k > best ? k : best;
+  for (size_t base = (size_t)blockIdx.x * kGemvThreads * kSelectPer; base < n;
+       base += (size_t)gridDim.x * kGemvThreads * kSelectPer) {
+    float v[kSelectPer];
+#pragma unroll
+    for (int u = 0; u < kSelectPer; ++u) v[u] = x[min(base + u * kGemvThreads + threadIdx.x, n - 1)];
+#pragma unroll
+    for (int u = 0; u < kSelectPer; ++u) {
+      const size_t i = base + u * kGemvThreads + threadIdx.x;
+      const uint64_t k = i < n ? select_key(v[u], (uint32_t)i) : 0ull;
+      best = k > best ? k : best;
+    }
   }
   select_publish_wave(best, sel, keys);
 }
@@ -439,6 +451,17 @@ hipError_t launch_gemv(hipStream_t st, GemvArgs& a) {
   return dispatch<EPI_PLAIN>(st, a, &blocks);
 }
 
+static hipError_t launch_finalize(hipStream_t st, const uint64_t* keys, uint32_t nkeys, uint32_t* token) {
+  const uint32_t per = (nkeys + kFinalizeThreads - 1) / kFinalizeThreads;  // keys per thread
+  if (per <= 1)
+    hipLaunchKernelGGL(select_finalize<1>, dim3(1), dim3(kFinalizeThreads), 0, st, keys, nkeys, token);
+  else if (per <= 8)
+    hipLaunchKernelGGL(select_finalize<8>, dim3(1), dim3(kFinalizeThreads), 0, st, keys, nkeys, token);
+  else
+    hipLaunchKernelGGL(select_finalize<48>, dim3(1), dim3(kFinalizeThreads), 0, st, keys, nkeys, token);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
   if (a.n[0] == 0) {
     hipLaunchKernelGGL(write_sentinel, dim3(1), dim3(64), 0, st, a.token);
@@ -447,8 +470,7 @@ hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
   uint32_t blocks = 0;
   hipError_t e = dispatch<EPI_ARGMAX>(st, a, &blocks);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kFinalizeThreads), 0, st, a.slots, blocks, a.token);
-  return hipGetLastError();
+  return launch_finalize(st, a.slots, blocks, a.token);
 }
 
 size_t argmax_keys_bound(size_t n) {
@@ -490,13 +512,12 @@ hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* key
     hipLaunchKernelGGL(write_sentinel, dim3(1), dim3(64), 0, st, token);
     return hipGetLastError();
   }
-  const uint64_t b = (n + kGemvThreads * 16 - 1) / (kGemvThreads * 16);
+  const uint64_t b = (n + kGemvThreads * kSelectPer - 1) / (kGemvThreads * kSelectPer);
   const unsigned blocks = (unsigned)(b > kSelectBlocks ? kSelectBlocks : b);
   hipLaunchKernelGGL(select_kernel, dim3(blocks), dim3(kGemvThreads), 0, st, x, n, keys);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(select_finalize, dim3(1), dim3(kFinalizeThreads), 0, st, keys, blocks, token);
-  return hipGetLastError();
+  return launch_finalize(st, keys, blocks, token);
 }
 
 }  // namespace w8a8
