@@ -95,6 +95,48 @@ def traffic_run() -> int:
     return 0
 
 
+def packed_head_setup(mod, s, hn):
+    """The reference model's BF16 head, packed: 4096 distinct rows of
+    N(0, 0.02) weights packed on the host, the packed rows replicated on the
+    device up to hn rows (every row streams from HBM; the exception list is
+    shared, so offsets repeat), and one activation row."""
+    from inferrous_amd import DeviceBuffer, PackedBf16, synth
+    from inferrous_amd import _lib as L
+    base_rows = 4096
+    wbase = (np.random.default_rng(46).standard_normal((base_rows, 4096)).astype(np.float32)
+             * np.float32(0.02)).view(np.uint32) >> 16
+    pk = PackedBf16.new(wbase.astype(np.uint16))
+    words = DeviceBuffer.zeroed(s, hn * 1536, np.uint32)
+    wb = DeviceBuffer.from_host(s, pk.words)
+    for r0 in range(0, hn, base_rows):
+        nr = min(base_rows, hn - r0)
+        L.check(L.lib().w8a8_memcpy_dtod(words.ptr + r0 * 1536 * 4, wb.ptr, nr * 1536 * 4, s.handle))
+    offs = DeviceBuffer.from_host(s, np.tile(pk.offsets.reshape(base_rows, 16), (hn // base_rows + 1, 1))[:hn]
+                                  .reshape(-1))
+    exc = DeviceBuffer.from_host(s, pk.exceptions)
+    hx = DeviceBuffer.from_host(s, synth.normal_rows(47, 1, 4096).reshape(-1))
+    logits = DeviceBuffer.zeroed(s, hn, np.float32)
+    s.synchronize()
+    return pk, words, offs, exc, hx, logits
+
+
+def head_profile_run() -> int:
+    """Workload for a kernel-trace profile of the packed BF16 head: 20 eager
+    head_packed + select_token passes over the 151,936-row head."""
+    from inferrous_amd import CudaContext, DeviceBuffer, load, synth
+    ctx = CudaContext(0)
+    mod = load(ctx)
+    s = ctx.new_stream()
+    pk, words, offs, exc, hx, logits = packed_head_setup(mod, s, synth.VOCAB)
+    token = DeviceBuffer.zeroed(s, 1, np.uint32)
+    for _ in range(20):
+        mod.head_packed(s, None, hx, words, offs, exc, logits)
+        mod.select_token(s, None, logits, token)
+    s.synchronize()
+    print("head profile done", flush=True)
+    return 0
+
+
 def prefill_profile_run() -> int:
     """Workload for a kernel-trace profile of the prefill GEMMs: 8 layers of
     distinct weights (1.5 GB, above the MALL), the four projections at
@@ -140,6 +182,8 @@ def main() -> int:
                     help="run only the counter-profiling workload (gate_up GEMVs + calibration copy)")
     ap.add_argument("--prefill-profile", action="store_true",
                     help="run only the prefill GEMM workload for a kernel-trace profile")
+    ap.add_argument("--head-profile", action="store_true",
+                    help="run only the packed BF16 head workload for a kernel-trace profile")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode "
@@ -151,6 +195,8 @@ def main() -> int:
         return traffic_run()
     if args.prefill_profile:
         return prefill_profile_run()
+    if args.head_profile:
+        return head_profile_run()
 
     from inferrous_amd import CudaContext, DeviceBuffer, Event, Graph, load, synth
 
@@ -387,27 +433,8 @@ def main() -> int:
         extras["producer_us_per_call"] = lat
         log(f"producers (us per call in a graph): {lat}")
         # the reference model's own head: BF16 151936 x 4096, losslessly packed
-        # (src/kernels.rs:2258-2373), then select_token.  4096 distinct rows of
-        # N(0, 0.02) weights are packed on the host and the packed rows are
-        # replicated on the device up to the vocabulary (every row streams
-        # from HBM; the exception list is shared, so offsets repeat).
-        from inferrous_amd import PackedBf16
-        from inferrous_amd import _lib as L
-        base_rows = 4096
-        wbase = (np.random.default_rng(46).standard_normal((base_rows, 4096)).astype(np.float32)
-                 * np.float32(0.02)).view(np.uint32) >> 16
-        pk = PackedBf16.new(wbase.astype(np.uint16))
-        words = DeviceBuffer.zeroed(s, hn * 1536, np.uint32)
-        wb = DeviceBuffer.from_host(s, pk.words)
-        for r0 in range(0, hn, base_rows):
-            nr = min(base_rows, hn - r0)
-            L.check(L.lib().w8a8_memcpy_dtod(words.ptr + r0 * 1536 * 4, wb.ptr, nr * 1536 * 4, s.handle))
-        offs = DeviceBuffer.from_host(s, np.tile(pk.offsets.reshape(base_rows, 16), (hn // base_rows + 1, 1))[:hn]
-                                      .reshape(-1))
-        exc = DeviceBuffer.from_host(s, pk.exceptions)
-        hx = DeviceBuffer.from_host(s, synth.normal_rows(47, 1, 4096).reshape(-1))
-        logits = DeviceBuffer.zeroed(s, hn, np.float32)
-        s.synchronize()
+        # (src/kernels.rs:2258-2373), then select_token.
+        pk, words, offs, exc, hx, logits = packed_head_setup(mod, s, hn)
         head_bytes = hn * 1536 * 4 + hn * 16 * 4 + 4096 * 4 + hn * 4
         t_head = time_graph(capture(lambda: mod.head_packed(s, None, hx, words, offs, exc, logits)), 20)
         t_sel = time_graph(capture(lambda: (mod.head_packed(s, None, hx, words, offs, exc, logits),
@@ -416,7 +443,7 @@ def main() -> int:
             "us": round(t_head * 1e3, 2), "GB/s": round(head_bytes / (t_head * 1e-3) / 1e9, 1),
             "pct_hbm_peak": round(head_bytes / (t_head * 1e-3) / 1e9 / HBM_PEAK_GBS * 100, 2),
             "us_with_select_token": round(t_sel * 1e3, 2), "bytes": head_bytes,
-            "escapes_per_value": round(pk.exceptions.size / wbase.size, 4),
+            "escapes_per_value": round(pk.exceptions.size / (4096 * 4096), 4),
             "reference_us": 574.0, "reference_hw": "RTX PRO 6000 Blackwell Max-Q, docs/qwen3-8b-w8a8/optimization/round-6.md:14"}
         log(f"packed BF16 head: {extras['bf16_packed_head']}")
         # prefill (config 4): M = 512 TOPS and M = 129 HBM GB/s, 36 layers x 4 shapes
