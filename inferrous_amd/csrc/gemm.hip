@@ -30,6 +30,10 @@
 //    Workgroups are numbered XCD-aware (below).  Tile shape per problem is
 //    chosen by the host from the tile count.  With a caller workspace, some
 //    shapes run split-K (i32 slabs + splitk_epilogue).
+//  * gemm_tall (128 < M <= 256, k % 128 == 0): one M tile holds every
+//    activation row, so each weight tile streams from HBM once; the eight
+//    waves are stacked along M and those past M only move data; activation
+//    rows past M are never loaded; split-K on narrow n.
 //  * gemm_skinny (small M on narrow n, HBM-bound, 16x16x64 MFMA): one
 //    workgroup owns 16 weight rows; its S waves split K and stream their
 //    weight fragments straight from HBM into MFMA B operands (no LDS round
