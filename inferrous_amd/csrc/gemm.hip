@@ -30,7 +30,8 @@
 //    Workgroups are numbered XCD-aware (below).  Tile shape per problem is
 //    chosen by the host from the tile count.  With a caller workspace, some
 //    shapes run split-K (i32 slabs + splitk_epilogue).
-//  * gemm_tall (128 < M <= 256, k % 128 == 0): one M tile holds every
+//  * gemm_tall (8 <= M <= 64 and 128 < M <= 256, k % 128 == 0; M tiles of
+//    64, 160 or 256 rows): one M tile holds every
 //    activation row, so each weight tile streams from HBM once; the eight
 //    waves are stacked along M and those past M only move data; activation
 //    rows past M are never loaded; split-K on narrow n.
@@ -533,7 +534,7 @@ __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
   }
 }
 
-// Prefill GEMM for 128 < M <= MA (gemm_tall, MA = 160 or 256).  One M tile
+// Prefill / small-batch GEMM for M <= MA (gemm_tall, MA = 64, 160 or 256).  One M tile
 // of MA rows holds every activation row, so each weight tile is read from
 // HBM once, and no DMA or MFMA goes to a second M tile holding a few rows.
 // The eight waves are stacked along M (wave w: rows 32w .. 32w + 31, all BN
@@ -759,13 +760,15 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, int& tile, uint32_t& 
   return kt % splits == 0 && kt / splits >= 4;
 }
 
-// gemm_tall plan for 128 < m <= 256 (measured on MI355X at M = 129 on the
-// Qwen3-8B projection shapes): 96-column tiles when they alone give about
-// one tile per CU; otherwise split K four ways (two when K is short), with
-// 96- or 64-column tiles, to reach about one workgroup per CU.  Returns
-// false when neither applies (the gemm_dma routes then run).
-static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits) {
-  if (m <= 128 || m > 256 || k % 128 != 0) return false;
+// gemm_tall plan for 8 <= m <= 64 and 128 < m <= 256 (measured on MI355X
+// on the Qwen3-8B projection shapes at M = 16, 64 and 129): 96-column tiles
+// when they alone give about one tile per CU; otherwise split K four ways
+// (two when K is short), with 96- or 64-column tiles, to reach about one
+// workgroup per CU.  Returns false when neither applies (the gemm_dma or
+// gemm_skinny routes then run).  ma: the M tile (64, 160 or 256 rows).
+static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits, int& ma) {
+  if (m < 8 || (m > 64 && m <= 128) || m > 256 || k % 128 != 0) return false;
+  ma = m <= 64 ? 64 : m <= 160 ? 160 : 256;
   const uint32_t kt = k / 128, t96 = (n + 95) / 96;
   if (t96 >= 224) {
     bn = 96;
@@ -782,7 +785,8 @@ static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& spl
 size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
   int tile;
   uint32_t splits;
-  if (tall_plan(m, n, k, tile, splits)) return splits > 1 ? (size_t)splits * m * n * sizeof(int32_t) : 0;
+  int ma;
+  if (tall_plan(m, n, k, tile, splits, ma)) return splits > 1 ? (size_t)splits * m * n * sizeof(int32_t) : 0;
   if (!split_plan(m, n, k, tile, splits)) return 0;
   return (size_t)splits * m * n * sizeof(int32_t);
 }
@@ -852,6 +856,18 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   // shapes: gate_up 24576 x 4096 at m = 16 / 32 / 64: 4.1 / 3.9 / 3.8 TB/s
   // against 3.4 / 2.3 / 1.5 TB/s).
   const bool wide = a.m >= 8 && a.k % 128 == 0 && (a.n + 127) / 128 >= 128;
+  {
+    int tile, ma;
+    uint32_t splits;
+    if (tall_plan(a.m, a.n, a.k, tile, splits, ma) &&
+        (splits == 1 || (a.partials && a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t)))) {
+      if (ma == 64)
+        return tile == 96 ? launch_tall<96, 4, 8, 64>(st, a, splits) : launch_tall<64, 4, 12, 64>(st, a, splits);
+      if (ma == 160)
+        return tile == 96 ? launch_tall<96, 4, 6, 160>(st, a, splits) : launch_tall<64, 4, 9, 160>(st, a, splits);
+      return tile == 96 ? launch_tall<96, 2, 8, 256>(st, a, splits) : launch_tall<64, 2, 12, 256>(st, a, splits);
+    }
+  }
   if (a.m <= 16 && !wide) {
     hipLaunchKernelGGL((gemm_skinny<1, 4, 4>), dim3(nb16, 1), dim3(256), 0, st, a);
   } else if (a.m <= 32 && !wide) {
@@ -861,13 +877,6 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   } else if (a.k % 128 == 0) {
     int tile;
     uint32_t splits;
-    if (tall_plan(a.m, a.n, a.k, tile, splits) &&
-        (splits == 1 || (a.partials && a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))))
-    {
-      if (a.m <= 160)
-        return tile == 96 ? launch_tall<96, 4, 6, 160>(st, a, splits) : launch_tall<64, 4, 9, 160>(st, a, splits);
-      return tile == 96 ? launch_tall<96, 2, 8, 256>(st, a, splits) : launch_tall<64, 2, 12, 256>(st, a, splits);
-    }
     if (a.partials && split_plan(a.m, a.n, a.k, tile, splits) &&
         a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))
       return tile == 0 ? launch_split<128, 128, 32, 64, 4, 4>(st, a, splits)
