@@ -850,11 +850,10 @@ static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   if (a.m == 0 || a.n == 0) return hipSuccess;
   const unsigned nb16 = (a.n + 15) / 16;
-  // Small m: from m = 8 the 8-wave kernel with 64-row tiles streams the
-  // weights faster when n gives at least 128 tiles; otherwise the skinny
-  // kernel's split-K keeps more CUs busy (measured on the decode/prefill
-  // shapes: gate_up 24576 x 4096 at m = 16 / 32 / 64: 4.1 / 3.9 / 3.8 TB/s
-  // against 3.4 / 2.3 / 1.5 TB/s).
+  // 8 <= m <= 64 and 128 < m <= 256 go to gemm_tall when its plan applies.
+  // Otherwise, for small m: from m = 8 the 8-wave kernel with 64-row tiles
+  // streams the weights faster when n gives at least 128 tiles; below that
+  // the skinny kernel's split-K keeps more CUs busy.
   const bool wide = a.m >= 8 && a.k % 128 == 0 && (a.n + 127) / 128 >= 128;
   {
     int tile, ma;
