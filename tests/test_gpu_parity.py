@@ -460,6 +460,43 @@ def test_linear_one_m_tile_wide_n(env, m, dtype, res):
         assert np.array_equal(bits(got), bits(of))
 
 
+@pytest.mark.parametrize("n,tile", [(23100, "256x192"), (15300, "128x192"), (6200, "128x128"), (1000, "128x64")])
+@pytest.mark.parametrize("dtype,res", [(np.uint16, True), (np.int32, False)])
+def test_linear_large_m_every_tile(env, n, tile, dtype, res):
+    """M = 300 (one full and one ragged 256-row tile; three 128-row tiles,
+    the last ragged) on the widths that select each gemm_dma tile, with a
+    ragged last column tile and K = 640 (five stages: both rings wrap)."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    m, k = 300, 640
+    print(f"large-M m={m} n={n} k={k} tile {tile} {np.dtype(dtype).name} res={res}", flush=True)
+    lib = _lib.lib()
+    assert lib.w8a8_linear_workspace_bytes(m, n, k) == 0  # no split-K plan: the tile route runs
+    rng = np.random.default_rng(n + 17)
+    q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    q[-1] = -127
+    w[-1] = 127
+    asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    resid = oracle.bf16_rne(rng.standard_normal(m * n).astype(F32))
+    dq, da, dw, dws, dres = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws), dev(s, resid)
+    dt = _lib.OUT_BF16 if dtype == np.uint16 else _lib.OUT_I32
+    out = DeviceBuffer.zeroed(s, m * n, dtype)
+    comb = DeviceBuffer.zeroed(s, m * n, dtype) if res else None
+    _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k,
+                                  dres.ptr if res else None, out.ptr,
+                                  comb.ptr if res else None, dt, _lib.PATH_AUTO, None, 0))
+    acc, of, ob = oracle.linear(q, asc, w, ws, k, threads=8)
+    got = out.to_host_vec(s)
+    if dtype == np.int32:
+        assert np.array_equal(got, acc)
+    else:
+        assert np.array_equal(got, ob)
+        want = (bits(oracle.residual(resid, of)) >> 16).astype(np.uint16)
+        assert np.array_equal(comb.to_host_vec(s), want)
+
+
 def test_linear_split_k_graph_replay(env):
     """The module's split-K workspace under graph capture: replays reuse the
     slabs and equal the eager result every time."""
