@@ -18,8 +18,9 @@
 //     16 x i32 result of lane l holds rows 8*(v/4)+4*(l/32)+v%4, column l%32.
 //
 // Kernels:
-//  * gemm_dma (M > 64, and 8 <= M <= 64 when n gives >= 128 tiles of 128
-//    columns; k % 128 == 0): the prefill GEMM, built on
+//  * gemm_dma (k % 128 == 0 and M > 64, or 8 <= M <= 64 when n gives >= 128
+//    tiles of 128 columns, wherever gemm_tall's plan does not apply): the
+//    prefill GEMM, built on
 //    v_mfma_i32_32x32x32_i8 (on gfx950 the 16x16x64 int8 form issues at half
 //    its rate), eight waves per workgroup (two per SIMD, so one wave's LDS
 //    reads overlap the other's MFMAs).  Operands move global -> LDS with
@@ -486,20 +487,34 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   store_blocks<EP, FM, FN>(a, acc, m0 + wm0, n0 + wn0, lane);
 }
 
+// The residual epilogue holds a residual per accumulator; with a 64 x 96
+// wave tile that is 96 more registers than the kernel has, and it spills.
+// Such tiles take no residual (launch_gemm routes residual outputs to
+// 128-row tiles).
+template <int WM, int WN>
+constexpr bool kResidualTile = WM * WN <= 32 * 96;
+
 template <int BM, int BN, int WM, int WN, int SA, int SB>
-static void launch_dma(hipStream_t st, const GemmArgs& a) {
+static hipError_t launch_dma(hipStream_t st, const GemmArgs& a) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
   const dim3 grid(tm * tn), block(512);
-  if (a.out_dtype == W8A8_OUT_I32)
+  if (a.residual) {
+    if constexpr (kResidualTile<WM, WN>) {
+      if (a.out_dtype == W8A8_OUT_F32)
+        hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32_RES>), grid, block, 0, st, a, tm, tn, 1u);
+      else
+        hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16_RES>), grid, block, 0, st, a, tm, tn, 1u);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (a.out_dtype == W8A8_OUT_I32) {
     hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32>), grid, block, 0, st, a, tm, tn, 1u);
-  else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32_RES>), grid, block, 0, st, a, tm, tn, 1u);
-  else if (a.out_dtype == W8A8_OUT_F32)
+  } else if (a.out_dtype == W8A8_OUT_F32) {
     hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32>), grid, block, 0, st, a, tm, tn, 1u);
-  else if (a.residual)
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16_RES>), grid, block, 0, st, a, tm, tn, 1u);
-  else
+  } else {
     hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16>), grid, block, 0, st, a, tm, tn, 1u);
+  }
+  return hipGetLastError();
 }
 
 // Cache policy of a load streamed once (the weights of a single M tile): the
@@ -883,18 +898,15 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
     // Tile per problem, measured on MI355X at M = 129 / 512 on the Qwen3-8B
     // projection shapes: the largest tile that still gives about one tile
     // per CU, smaller tiles for narrow N.
+    // Residual outputs skip the 256 x 192 tile (kResidualTile); t128 is
+    // then at least 480.
     const uint64_t t256 = (uint64_t)((a.m + 255) / 256) * ((a.n + 191) / 192);
     const uint64_t t128 = (uint64_t)((a.m + 127) / 128) * ((a.n + 191) / 192);
-    if (t256 >= 240)
-      launch_dma<256, 192, 64, 96, 2, 3>(st, a);
-    else if (t128 >= 240)
-      launch_dma<128, 192, 32, 96, 2, 4>(st, a);
-    else if (a.n >= 6144 && a.m >= 256)
-      launch_dma<128, 128, 32, 64, 4, 4>(st, a);
-    else if (a.m >= 128)
-      launch_dma<128, 64, 32, 32, 4, 4>(st, a);
-    else
-      launch_dma<64, 128, 32, 32, 4, 4>(st, a);
+    if (t256 >= 240 && !a.residual) return launch_dma<256, 192, 64, 96, 2, 3>(st, a);
+    if (t128 >= 240) return launch_dma<128, 192, 32, 96, 2, 4>(st, a);
+    if (a.n >= 6144 && a.m >= 256) return launch_dma<128, 128, 32, 64, 4, 4>(st, a);
+    if (a.m >= 128) return launch_dma<128, 64, 32, 32, 4, 4>(st, a);
+    return launch_dma<64, 128, 32, 32, 4, 4>(st, a);
   } else {
     constexpr int BM = 128, BN = 128;
     const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;

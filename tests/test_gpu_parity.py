@@ -465,7 +465,8 @@ def test_linear_one_m_tile_wide_n(env, m, dtype, res):
 def test_linear_large_m_every_tile(env, n, tile, dtype, res):
     """M = 300 (one full and one ragged 256-row tile; three 128-row tiles,
     the last ragged) on the widths that select each gemm_dma tile, with a
-    ragged last column tile and K = 640 (five stages: both rings wrap)."""
+    ragged last column tile and K = 640 (five stages: both rings wrap).
+    Residual outputs of the 256x192 width take the 128x192 tile."""
     from inferrous_amd import _lib
     ctx, mod, s = env
     m, k = 300, 640
