@@ -558,12 +558,17 @@ __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
 // Rings as in gemm_dma: activations (SA slots of MA rows; the lines are
 // shared by every workgroup and come from L2 or MALL) and weights (SB slots;
 // the lines come from HBM and are read once, non-temporal).  With few MFMAs
-// per stage the stage is short, so both rings look several stages ahead.  A
-// stage's DMA instructions (8 rows x 128 bytes each) are dealt to the waves
-// round-robin, separately for the ceil(M / 8) activation row groups -- rows
-// past the last group are never loaded -- and the BN / 8 weight row groups,
-// so a wave issues na activation and nb weight instructions per stage and
-// counts its waits with its own na, nb.  During stage kt it issues
+// per stage the stage is short, so both rings look several stages ahead.
+// Loads complete in issue order, so a weight load issued before an
+// activation load has to land before that activation's wait: weight slots
+// beyond the activation ring's depth add no lookahead, and most plans use
+// equal depths.
+//
+// A stage's DMA instructions (8 rows x 128 bytes each) are dealt to the
+// waves round-robin, separately for the ceil(M / 8) activation row groups --
+// rows past the last group are never loaded -- and the BN / 8 weight row
+// groups, so a wave issues na activation and nb weight instructions per stage
+// and counts its waits with its own na, nb.  During stage kt it issues
 // A(kt + SA - 1), then B(kt + SB - 1).
 // Split-K as in gemm_dma: workgroup (tile, split) writes i32 slab `split`.
 template <int BN, int SA, int SB, int MA, int EP>
@@ -573,8 +578,9 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
   constexpr uint32_t NB = BN / 8;
   constexpr int kMaxA = (MA / 8 + 7) / 8, kMaxB = (NB + 7) / 8;
   static_assert(BN % 32 == 0 && BN <= 128 && MA % 32 == 0 && MA <= 256, "tile");
-  static_assert(SA >= 2 && SB > SA && SA * ASL + SB * BSL <= 160 * 1024, "LDS");
-  static_assert(kMaxB + (SA - 2) * (kMaxA + kMaxB) <= 20 && (SA - 2) * kMaxA + (SB - 2) * kMaxB <= 20,
+  static_assert(SA >= 2 && SB >= SA && SA * ASL + SB * BSL <= 160 * 1024, "LDS");
+  static_assert((SB > SA ? kMaxB : 0) + (SA - 2) * (kMaxA + kMaxB) <= 20 &&
+                    (SA - 2) * kMaxA + (SB - 2) * kMaxB <= 20,
                 "wait range");
   __shared__ __attribute__((aligned(1024))) int8_t lds[SA * ASL + SB * BSL];
   int8_t* const ldsA = lds;
@@ -630,9 +636,10 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
     if (kt + SB - 1 < KT) issueB(kt + SB - 1);
   };
   // end of stage kt: A(kt + 1) and B(kt + 1) landed; in flight may remain the
-  // B half of A(kt + 1)'s batch and the SA - 2 whole batches after it
+  // B half of A(kt + 1)'s batch (when SB > SA) and the SA - 2 whole batches
+  // after it
   auto wait_next = [&](uint32_t kt) {
-    if (kt + SB - 1 < KT) wait_vmcnt_dyn(nb + (SA - 2) * (na + nb));
+    if (kt + SB - 1 < KT) wait_vmcnt_dyn((SB > SA ? nb : 0) + (SA - 2) * (na + nb));
     else wait_vmcnt<0>();
   };
 
@@ -876,10 +883,10 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
     if (tall_plan(a.m, a.n, a.k, tile, splits, ma) &&
         (splits == 1 || (a.partials && a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t)))) {
       if (ma == 64)
-        return tile == 96 ? launch_tall<96, 4, 8, 64>(st, a, splits) : launch_tall<64, 4, 12, 64>(st, a, splits);
+        return tile == 96 ? launch_tall<96, 4, 8, 64>(st, a, splits) : launch_tall<64, 8, 8, 64>(st, a, splits);
       if (ma == 160)
-        return tile == 96 ? launch_tall<96, 4, 6, 160>(st, a, splits) : launch_tall<64, 4, 9, 160>(st, a, splits);
-      return tile == 96 ? launch_tall<96, 2, 8, 256>(st, a, splits) : launch_tall<64, 2, 12, 256>(st, a, splits);
+        return tile == 96 ? launch_tall<96, 4, 6, 160>(st, a, splits) : launch_tall<64, 5, 5, 160>(st, a, splits);
+      return tile == 96 ? launch_tall<96, 3, 3, 256>(st, a, splits) : launch_tall<64, 4, 4, 256>(st, a, splits);
     }
   }
   if (a.m <= 16 && !wide) {
