@@ -171,6 +171,43 @@ def prefill_profile_run() -> int:
     return 0
 
 
+def ragged_profile_run() -> int:
+    """Workload for a kernel-trace profile of the ragged small batches
+    (config 5): 8 layers of distinct gate_up and down weights (1.2 GB), M = 4,
+    16 and 64 per-row-seeded rows, the dot4 GEMV and the MFMA GEMM forced in
+    turn, three eager passes each (no graphs)."""
+    from inferrous_amd import CudaContext, DeviceBuffer, load, synth
+    ctx = CudaContext(0)
+    mod = load(ctx)
+    s = ctx.new_stream()
+    nl = 8
+    mats = []
+    for layer in range(nl):
+        for si in (2, 3):
+            name, n, k = synth.DECODE_SHAPES[si]
+            w = DeviceBuffer.zeroed(s, n * k, np.int8)
+            ws = DeviceBuffer.zeroed(s, n, np.float32)
+            mod.synth_i8(s, w, SEED_W, synth.weight_stream(layer, si))
+            mod.synth_f32(s, ws, SEED_S, synth.scale_stream(layer, si), 1e-3, 1e-2)
+            mats.append((name, n, k, w, ws))
+    for m in (4, 16, 64):
+        pq, outs = {}, {}
+        for (name, n, k, _, _) in mats[:2]:
+            x = synth.ragged_rows(range(9000 + 100 * m, 9000 + 100 * m + m), k).reshape(-1)
+            q = DeviceBuffer.zeroed(s, m * k, np.int8)
+            sc = DeviceBuffer.zeroed(s, m, np.float32)
+            mod.quantize(s, None, DeviceBuffer.from_host(s, x), k, q, sc)
+            pq[k] = (q, sc)
+            outs[name] = DeviceBuffer.zeroed(s, m * n, np.uint16)
+        for fam in ("linear_dot4", "linear_mfma"):
+            for _ in range(3):
+                for (name, n, k, w, ws) in mats:
+                    getattr(mod, fam)(s, None, pq[k][0], pq[k][1], w, ws, k, outs[name])
+            s.synchronize()
+            print(f"ragged M={m} {fam} done", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,6 +221,8 @@ def main() -> int:
                     help="run only the prefill GEMM workload for a kernel-trace profile")
     ap.add_argument("--head-profile", action="store_true",
                     help="run only the packed BF16 head workload for a kernel-trace profile")
+    ap.add_argument("--ragged-profile", action="store_true",
+                    help="run only the ragged small-batch workload for a kernel-trace profile")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode "
@@ -197,6 +236,8 @@ def main() -> int:
         return prefill_profile_run()
     if args.head_profile:
         return head_profile_run()
+    if args.ragged_profile:
+        return ragged_profile_run()
 
     from inferrous_amd import CudaContext, DeviceBuffer, Event, Graph, load, synth
 
