@@ -27,6 +27,26 @@ def test_header_declarations_match_binding():
     assert declared_symbols() == set(_lib.SIGNATURES)
 
 
+def declared_arity() -> dict[str, int]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(w8a8_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_integration_rust_binding_covers_header():
+    """The Rust FFI block a maintainer would add binds every declared entry
+    point, each with the header's number of parameters."""
+    doc = (ROOT / "INTEGRATION.md").read_text()
+    bound = {}
+    for name, params in re.findall(r"pub fn (w8a8_[a-z0-9_]+)\(([^)]*)\)", doc, flags=re.S):
+        params = re.sub(r"//[^\n]*", "", params).strip()
+        bound[name] = 0 if not params else params.count(",") + 1
+    assert bound == declared_arity()
+
+
 def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
                          capture_output=True, text=True, check=True).stdout
