@@ -96,27 +96,30 @@ __device__ __forceinline__ int owner(const GemvArgs& a, uint32_t g) {
 // one-workgroup kernel, stream-ordered after the producer, reduces the keys
 // and writes the token.  Each call writes every key it reads, so the
 // workspace needs no initialisation and carries nothing between calls.
+template <int W = kGemvWaves>
 struct SelectLds {
-  uint64_t key[kGemvWaves];
+  uint64_t key[W];
   uint32_t arrived;
 };
 
-__device__ __forceinline__ void select_lds_init(SelectLds& s) {
+template <int W>
+__device__ __forceinline__ void select_lds_init(SelectLds<W>& s) {
   if (threadIdx.x == 0) s.arrived = 0;
   __syncthreads();
 }
 
 // Every lane of every wave calls this once, with its key (0 for no row).
-__device__ __forceinline__ void select_publish_wave(uint64_t key, SelectLds& s, uint64_t* keys) {
+template <int W>
+__device__ __forceinline__ void select_publish_wave(uint64_t key, SelectLds<W>& s, uint64_t* keys) {
   key = wave_max_u64(key);
   if ((threadIdx.x & 63) == 0) {
     s.key[threadIdx.x >> 6] = key;
     const uint32_t before =
         __hip_atomic_fetch_add(&s.arrived, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (before == kGemvWaves - 1) {
+    if (before == W - 1) {
       uint64_t b = s.key[0];
 #pragma unroll
-      for (int i = 1; i < kGemvWaves; ++i) b = s.key[i] > b ? s.key[i] : b;
+      for (int i = 1; i < W; ++i) b = s.key[i] > b ? s.key[i] : b;
       keys[blockIdx.x] = b;
     }
   }
@@ -151,16 +154,17 @@ __global__ __launch_bounds__(kFinalizeThreads) void select_finalize(const uint64
 }
 
 // M = 1, k = KC * 1024 known at compile time: activations held in registers.
-template <int R, int KC, int EPI>
-__global__ __launch_bounds__(kGemvThreads) void gemv_m1(GemvArgs a) {
+// WV waves per workgroup.
+template <int R, int KC, int EPI, int WV = kGemvWaves>
+__global__ __launch_bounds__(64 * WV) void gemv_m1(GemvArgs a) {
   const int lane = threadIdx.x & 63;
-  const uint32_t g = blockIdx.x * kGemvWaves + wave_id();
+  const uint32_t g = blockIdx.x * WV + wave_id();
   const bool live = g < a.gbegin[a.count];
   const int mi = live ? owner(a, g) : 0;
   const uint32_t n = a.n[mi];
   const uint32_t row0 = live ? (g - a.gbegin[mi]) * R : 0;
   constexpr uint32_t K = KC * 1024;
-  __shared__ SelectLds sel;
+  __shared__ SelectLds<WV> sel;
   if (EPI == EPI_ARGMAX) select_lds_init(sel);
 
   int acc[R];
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
   const uint32_t row0 = live ? (g - a.gbegin[mi]) * R : 0;
   const uint32_t m0 = blockIdx.y * MT;
   const uint32_t K = a.k;
-  __shared__ SelectLds sel;
+  __shared__ SelectLds<> sel;
   if (EPI == EPI_ARGMAX) select_lds_init(sel);
 
   int acc[V];
@@ -370,7 +374,7 @@ constexpr int kSelectPer = 16;
 
 __global__ __launch_bounds__(kGemvThreads) void select_kernel(const float* __restrict__ x, size_t n,
                                                                uint64_t* keys) {
-  __shared__ SelectLds sel;
+  __shared__ SelectLds<> sel;
   select_lds_init(sel);
   uint64_t best = 0;
   for (size_t base = (size_t)blockIdx.x * kGemvThreads * kSelectPer; base < n;
@@ -406,12 +410,16 @@ static uint32_t count_groups(GemvArgs& a, const uint32_t* n, int count) {
 
 // Each launcher reports its grid's x extent in *blocks (the selection
 // finalize reads one key per workgroup).
+// The fused selection publishes one key per workgroup, and the one-workgroup
+// finalize reads them all: its workgroups carry 16 waves, a quarter of the
+// keys.
 template <int R, int KC, int EPI>
 static hipError_t launch_m1(hipStream_t st, GemvArgs& a, const uint32_t* nn, uint32_t* blocks) {
+  constexpr int W = EPI == EPI_ARGMAX ? 16 : kGemvWaves;
   const uint32_t groups = count_groups<R>(a, nn, a.count);
-  *blocks = (groups + kGemvWaves - 1) / kGemvWaves;
+  *blocks = (groups + W - 1) / W;
   if (groups == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemv_m1<R, KC, EPI>), dim3(*blocks), dim3(kGemvThreads), 0, st, a);
+  hipLaunchKernelGGL((gemv_m1<R, KC, EPI, W>), dim3(*blocks), dim3(64 * W), 0, st, a);
   return hipGetLastError();
 }
 
@@ -457,6 +465,8 @@ static hipError_t launch_finalize(hipStream_t st, const uint64_t* keys, uint32_t
     hipLaunchKernelGGL(select_finalize<1>, dim3(1), dim3(kFinalizeThreads), 0, st, keys, nkeys, token);
   else if (per <= 8)
     hipLaunchKernelGGL(select_finalize<8>, dim3(1), dim3(kFinalizeThreads), 0, st, keys, nkeys, token);
+  else if (per <= 16)
+    hipLaunchKernelGGL(select_finalize<16>, dim3(1), dim3(kFinalizeThreads), 0, st, keys, nkeys, token);
   else
     hipLaunchKernelGGL(select_finalize<48>, dim3(1), dim3(kFinalizeThreads), 0, st, keys, nkeys, token);
   return hipGetLastError();
@@ -474,7 +484,8 @@ hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
 }
 
 size_t argmax_keys_bound(size_t n) {
-  // every route puts at least one row per wave and kGemvWaves waves per workgroup
+  // every route puts at least one row per wave and at least kGemvWaves waves
+  // per workgroup
   return (n + kGemvWaves - 1) / kGemvWaves;
 }
 
