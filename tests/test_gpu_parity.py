@@ -280,6 +280,32 @@ def test_linear_argmax_fused(env, k):
     assert (tok2 == 0xFFFFFFFF) == (not np.all(np.isfinite(lg2)))
 
 
+@pytest.mark.parametrize("k,n", [(4096, 4099), (4096, 5), (12288, 1001), (12288, 17), (4096, 1)])
+def test_linear_argmax_partial_last_workgroup(env, k, n):
+    """Row counts that leave the last selection workgroup partly empty (its
+    waves past the last row publish no key): the maximum in the last row,
+    then tied with row 0."""
+    ctx, mod, s = env
+    print(f"argmax partial k={k} n={n}", flush=True)
+    rng = np.random.default_rng(k + n)
+    q = rng.integers(-127, 128, size=k, dtype=np.int8)
+    w = rng.integers(-64, 65, size=(n, k), dtype=np.int8)
+    w[n - 1] = 127 * np.sign(q).astype(np.int8)
+    ws = np.full(n, 0.004, F32)
+    asc = np.array([0.01], F32)
+    dq, da, dws = dev(s, q), dev(s, asc), dev(s, ws)
+    for tie in (False, True):
+        if tie:
+            w[0] = w[n - 1]
+        tok, logits = oracle.linear_argmax(q, asc, w, ws, k)
+        assert tok == (0 if tie else n - 1)
+        t = DeviceBuffer.zeroed(s, 1, np.uint32)
+        lg = DeviceBuffer.zeroed(s, n, np.float32)
+        mod.linear_argmax(s, dq, da, dev(s, w), dws, k, t, lg)
+        assert int(t.to_host_vec(s)[0]) == tok, tie
+        assert np.array_equal(bits(lg.to_host_vec(s)), bits(logits))
+
+
 def test_linear_argmax_consecutive_calls_smaller_max(env):
     """The selection slots are reused across calls: a call whose maximum is
     far below the previous call's must still find its own token."""
