@@ -408,11 +408,10 @@ static uint32_t count_groups(GemvArgs& a, const uint32_t* n, int count) {
   return g;
 }
 
-// Each launcher reports its grid's x extent in *blocks (the selection
-// finalize reads one key per workgroup).
-// The fused selection publishes one key per workgroup, and the one-workgroup
-// finalize reads them all: its workgroups carry 16 waves, a quarter of the
-// keys.
+// Each launcher reports its grid's x extent in *blocks: the fused selection
+// publishes one key per workgroup, and the one-workgroup finalize reads them
+// all.  Its M = 1 workgroups carry 16 waves, a quarter of the keys of the
+// plain GEMV's 4-wave workgroups.
 template <int R, int KC, int EPI>
 static hipError_t launch_m1(hipStream_t st, GemvArgs& a, const uint32_t* nn, uint32_t* blocks) {
   constexpr int W = EPI == EPI_ARGMAX ? 16 : kGemvWaves;
