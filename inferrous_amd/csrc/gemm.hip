@@ -498,7 +498,9 @@ template <int BM, int BN, int WM, int WN, int SA, int SB>
 static hipError_t launch_dma(hipStream_t st, const GemmArgs& a) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
   const dim3 grid(tm * tn), block(512);
-  if (a.residual) {
+  if (a.out_dtype == W8A8_OUT_I32) {
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32>), grid, block, 0, st, a, tm, tn, 1u);
+  } else if (a.residual) {
     if constexpr (kResidualTile<WM, WN>) {
       if (a.out_dtype == W8A8_OUT_F32)
         hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32_RES>), grid, block, 0, st, a, tm, tn, 1u);
@@ -507,8 +509,6 @@ static hipError_t launch_dma(hipStream_t st, const GemmArgs& a) {
     } else {
       return hipErrorInvalidValue;
     }
-  } else if (a.out_dtype == W8A8_OUT_I32) {
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32>), grid, block, 0, st, a, tm, tn, 1u);
   } else if (a.out_dtype == W8A8_OUT_F32) {
     hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32>), grid, block, 0, st, a, tm, tn, 1u);
   } else {
