@@ -575,6 +575,7 @@ def cpu_baseline() -> dict:
         mats.append((n, k, w, ws))
     xs = {4096: synth.normal_rows(40, 1, 4096).reshape(-1), 12288: synth.normal_rows(41, 1, 12288).reshape(-1)}
     sample_bytes = sum(gemv_bytes(n, k) for (n, k, _, _) in mats)
+    sample_ops = sum(2 * n * k for (n, k, _, _) in mats)
     log(f"cpu baseline: host weights ready in {time.time() - t0:.1f}s")
 
     def one_pass(threads: int) -> float:
@@ -584,7 +585,7 @@ def cpu_baseline() -> dict:
             oracle.linear(q, sc, w, ws, k, threads=threads)
         return time.perf_counter() - t
 
-    res = {}
+    res, gops = {}, {}
     for threads in sorted({nthreads, 8, 1}, reverse=True):
         one_pass(threads)
         times = []
@@ -593,6 +594,7 @@ def cpu_baseline() -> dict:
             times.append(one_pass(threads))
         med = float(np.median(times))
         res[threads] = sample_bytes / med / 1e9
+        gops[threads] = sample_ops / med / 1e9
         log(f"cpu baseline {threads} threads: {med * 1e3:.1f} ms/pass, {res[threads]:.2f} GB/s")
     cpu_model = ""
     try:
@@ -605,9 +607,10 @@ def cpu_baseline() -> dict:
     return {"value": round(res[nthreads], 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
             "sample": (f"C oracle (quantize + int32 GEMV + BF16 epilogue) over layer 0's qkv/o/"
                        f"gate_up/down at M=1 ({sample_bytes / 1e6:.1f} MB per pass), median of >=5 "
-                       f"passes; {cpu_model}; GB/s at 8 threads {res.get(8, 0):.3f}, at 1 thread "
-                       f"{res.get(1, 0):.3f}"),
-            "gbs_by_threads": {str(t): round(v, 3) for t, v in res.items()}}
+                       f"passes; {cpu_model}, {os.cpu_count()} logical CPUs; GB/s at 8 threads "
+                       f"{res.get(8, 0):.3f}, at 1 thread {res.get(1, 0):.3f}"),
+            "gbs_by_threads": {str(t): round(v, 3) for t, v in res.items()},
+            "gops_by_threads": {str(t): round(v, 3) for t, v in gops.items()}}
 
 
 if __name__ == "__main__":
