@@ -397,7 +397,8 @@ def test_errors_raise_not_fall_back(env):
 # ------------------------------------------------------------------ split-K workspace
 @pytest.mark.parametrize("m,n,k", [(129, 4096, 12288), (512, 4096, 12288), (129, 4096, 4096), (129, 6144, 4096),
                                    (16, 4096, 12288), (64, 4096, 12288), (40, 6144, 4096),
-                                   (100, 96, 12288), (255, 1024, 4096)])
+                                   (100, 96, 12288), (255, 1024, 4096),
+                                   (129, 4100, 4096), (64, 4100, 12288), (512, 4100, 12288)])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     """w8a8_linear_ex with a workspace (split-K partials + exact i32 epilogue)
@@ -441,6 +442,36 @@ def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
         assert np.array_equal(outs[0][1], want)
     else:
         assert np.array_equal(bits(got), bits(of))
+
+
+def test_linear_split_k_unaligned_outputs(env):
+    """The split-K epilogue at outputs, residuals and scales that do not start
+    on 16 bytes (offset views inside larger buffers): the 4-column epilogue
+    runs in place of the 16-byte one, with the same bits."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    lib = _lib.lib()
+    m, n, k = 129, 4096, 12288
+    need = lib.w8a8_linear_workspace_bytes(m, n, k)
+    assert need > 0
+    rng = np.random.default_rng(4242)
+    q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    resid = oracle.bf16_rne(rng.standard_normal(m * n).astype(F32))
+    acc, of, ob = oracle.linear(q, asc, w, ws, k, threads=8)
+    want_comb = (bits(oracle.residual(resid, of)) >> 16).astype(np.uint16)
+    dq, da, dw = dev(s, q), dev(s, asc), dev(s, w)
+    dws = dev(s, np.concatenate([np.zeros(1, F32), ws]))          # ws at +4 bytes
+    dres = dev(s, np.concatenate([np.zeros(1, F32), resid]))      # residual at +4 bytes
+    work = DeviceBuffer.zeroed(s, need, np.uint8)
+    out = DeviceBuffer.zeroed(s, m * n + 1, np.uint16)              # outputs at +2 bytes
+    comb = DeviceBuffer.zeroed(s, m * n + 1, np.uint16)
+    _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr + 4, n, k, dres.ptr + 4,
+                                  out.ptr + 2, comb.ptr + 2, _lib.OUT_BF16, _lib.PATH_AUTO, work.ptr, need))
+    assert np.array_equal(out.to_host_vec(s)[1:], ob)
+    assert np.array_equal(comb.to_host_vec(s)[1:], want_comb)
 
 
 @pytest.mark.parametrize("m", [8, 33, 64, 129, 193, 256])
