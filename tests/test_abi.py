@@ -7,6 +7,7 @@ from __future__ import annotations
 import ctypes
 import re
 import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -251,3 +252,13 @@ def test_head_entries_validation():
     assert L.w8a8_unpack_bf16(None, A, A, A, 256, A) == _lib.EINIT
     assert L.w8a8_unpack_bf16(None, A, A, A, 255, A) == _lib.ESHAPE
     assert L.w8a8_unpack_bf16(None, A, A, A, 256, A + 1) == _lib.EALIGN
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and a message,
+    before anything touches a device."""
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+    assert r.stdout == ""
