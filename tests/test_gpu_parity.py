@@ -444,6 +444,44 @@ def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
         assert np.array_equal(bits(got), bits(of))
 
 
+def test_large_row_counts_beyond_grid_y(env):
+    """More rows than a grid's y extent holds (65,535): the quantizer over
+    70,000 rows, and a split-K GEMM whose epilogue loops its rows
+    (M = 70,000, K = 8192, residual), both bit-exact."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    print("large rows: quantize 70000 x 32, then split-K linear m=70000 n=64 k=8192", flush=True)
+    lib = _lib.lib()
+    rows_, width = 70000, 32
+    rng = np.random.default_rng(70000)
+    x = rng.standard_normal(rows_ * width).astype(F32)
+    q = DeviceBuffer.zeroed(s, rows_ * width, np.int8)
+    sc = DeviceBuffer.zeroed(s, rows_, np.float32)
+    dx = dev(s, x)
+    mod.quantize(s, None, dx, width, q, sc)
+    wq, wsc = oracle.quantize(x, width)
+    assert np.array_equal(q.to_host_vec(s), wq)
+    assert np.array_equal(bits(sc.to_host_vec(s)), bits(wsc))
+    m, n, k = 70000, 64, 8192
+    need = lib.w8a8_linear_workspace_bytes(m, n, k)
+    assert need > 0  # the split-K plan runs
+    qa = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    resid = oracle.bf16_rne(rng.standard_normal(m * n).astype(F32))
+    acc, of, ob = oracle.linear(qa, asc, w, ws, k, threads=8)
+    out = DeviceBuffer.zeroed(s, m * n, np.uint16)
+    comb = DeviceBuffer.zeroed(s, m * n, np.uint16)
+    work = DeviceBuffer.zeroed(s, need, np.uint8)
+    # named, so that no buffer is freed before the kernels that read it ran
+    dq, da, dw, dws, dres = dev(s, qa), dev(s, asc), dev(s, w), dev(s, ws), dev(s, resid)
+    _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k, dres.ptr, out.ptr,
+                                  comb.ptr, _lib.OUT_BF16, _lib.PATH_AUTO, work.ptr, need))
+    assert np.array_equal(out.to_host_vec(s), ob)
+    assert np.array_equal(comb.to_host_vec(s), (bits(oracle.residual(resid, of)) >> 16).astype(np.uint16))
+
+
 def test_linear_split_k_unaligned_outputs(env):
     """The split-K epilogue at outputs, residuals and scales that do not start
     on 16 bytes (offset views inside larger buffers): the 4-column epilogue
