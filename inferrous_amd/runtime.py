@@ -237,6 +237,8 @@ class Graph:
         if exc_type is None:
             check(st, "capture end")
             self._p = p.value
+        elif st == 0 and p.value:
+            lib().w8a8_graph_destroy(p.value)   # capture abandoned by the exception
         return False
 
     def launch(self, stream: CudaStream | None = None) -> None:

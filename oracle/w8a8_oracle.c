@@ -345,6 +345,8 @@ uint64_t orc_synth_hash(uint64_t seed, uint64_t stream, uint64_t index) {
  * (src/model.rs:143 forbids -128). */
 void orc_synth_i8(uint64_t seed, uint64_t stream, uint64_t first, size_t n,
                   int8_t *out) {
+  /* element-wise, so the parallel split cannot change a value */
+#pragma omp parallel for schedule(static) if (n >= (1u << 20))
   for (size_t j = 0; j < n; ++j) {
     uint64_t i = first + j;
     uint64_t h = orc_synth_hash(seed, stream, i >> 2);

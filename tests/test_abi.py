@@ -262,3 +262,40 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2
     assert "one GPU" in r.stderr
     assert r.stdout == ""
+
+
+def _fake(n, dtype):
+    """A DeviceBuffer-shaped object for host-side validation only: a fake
+    aligned address that no call reaches, since the checks raise first."""
+    import numpy as np
+
+    from inferrous_amd import DeviceBuffer
+    b = DeviceBuffer.__new__(DeviceBuffer)
+    b.dtype, b.n = np.dtype(dtype), int(n)
+    b.nbytes = b.n * b.dtype.itemsize
+    b._p, b._base = A, object()     # a view: never freed
+    return b
+
+
+def test_module_grouped_and_swiglu_check_operand_lengths():
+    """Short q or weight buffers raise ValueError before the library is
+    called, for every member of a group and both SwiGLU matrices."""
+    import numpy as np
+
+    from inferrous_amd import LoadedModule
+    mod = LoadedModule(None)
+    m, k, n = 2, 64, 8
+    q, asc = _fake(m * k, np.int8), _fake(m, np.float32)
+    ws, out = _fake(n, np.float32), _fake(m * n, np.float32)
+    good, short = _fake(n * k, np.int8), _fake(n * k - 1, np.int8)
+    with pytest.raises(ValueError, match="q"):
+        mod.linear_grouped(None, _fake(m * k - 16, np.int8), asc, k, [(good, ws, out)])
+    with pytest.raises(ValueError, match=r"w\[2\]"):
+        mod.linear_triple(None, None, q, asc, k, good, ws, out, good, ws, out, short, ws, out)
+    with pytest.raises(ValueError, match="w_up"):
+        mod.linear_swiglu(None, None, q, asc, k, good, ws, out, short, ws, out, out, None)
+    with pytest.raises(ValueError, match="w_gate"):
+        mod.linear_swiglu(None, None, q, asc, k, short, ws, out, good, ws, out, out, None)
+    with pytest.raises(ValueError, match="q"):
+        mod.linear_swiglu(None, None, _fake(k, np.int8), asc, k, good, ws, out, good, ws, out, out, None)
+

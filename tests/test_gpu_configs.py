@@ -3,8 +3,9 @@ W8A8 baseline), on the same seeded synthetic tensors the bench uses.
 
 Weights are generated on the device; the checker regenerates the same rows
 on the host (oracle.synth_*), so full matrices are compared where the CPU
-oracle finishes in seconds and sampled rows elsewhere, plus size-independent
-properties (a row-sum identity over every output of the 36-layer set).
+oracle finishes in seconds (every output of the 36-layer decode set and of
+the lm_head) and sampled rows plus a row-sum identity for the prefill
+shapes.
 """
 from __future__ import annotations
 
@@ -81,10 +82,10 @@ def test_config1_single_linear_full(env):
 
 
 def test_config2_decode_layer_set(env):
-    """36 layers x {qkv, o, gate_up, down} at M=1: sampled rows exact, and
-    for every output the identity sum_c acc[c] == q . colsum(W) holds."""
+    """36 layers x {qkv, o, gate_up, down} at M=1, every output of every
+    layer: the i32 accumulators and the BF16 outputs equal the oracle's on
+    the host-regenerated weights (7 GB of int8 regenerated layer by layer)."""
     ctx, mod, s = env
-    rng = np.random.default_rng(2)
     xs = {4096: synth.normal_rows(40, 1, 4096), 12288: synth.normal_rows(41, 1, 12288)}
     qs = {k: quantize_dev(mod, s, x, k) for k, x in xs.items()}
     for layer in range(36):
@@ -96,17 +97,11 @@ def test_config2_decode_layer_set(env):
             mod.linear(s, None, q, sc, w, ws, k, o32)
             ob = DeviceBuffer.zeroed(s, n, np.uint16)
             mod.linear(s, None, q, sc, w, ws, k, ob)
-            acc, outb = o32.to_host_vec(s), ob.to_host_vec(s)
-            pick = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, 14)]))
-            hw, hws = host_weights(n, k, ws_id, ss_id, pick)
+            hw, hws = host_weights(n, k, ws_id, ss_id)
             a2, _, b2 = oracle.linear(hq, hsc, hw, hws, k)
-            assert np.array_equal(acc[pick], a2), (layer, name)
-            assert np.array_equal(outb[pick], b2), (layer, name)
-            if layer % 12 == 0:  # full-matrix identity on a third of the layers
-                hw_all, _ = host_weights(n, k, ws_id, ss_id)
-                col = hw_all.astype(np.int64).sum(0)
-                assert int(acc.astype(np.int64).sum()) == int(hq.astype(np.int64)[0] @ col)
-            del w, ws
+            assert np.array_equal(o32.to_host_vec(s), a2), (layer, name)
+            assert np.array_equal(ob.to_host_vec(s), b2), (layer, name)
+            del w, ws, hw
 
 
 def test_config3_lm_head_argmax_full(env):

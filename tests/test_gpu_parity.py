@@ -112,18 +112,22 @@ def test_quantize_widths_edges_and_bf16(env, width):
 
 
 # ------------------------------------------------------------------ linear
-LINEAR_OPS = ("linear", "linear_dot4", "linear_mfma", "linear_prefill", "linear_splitk",
-              "linear_tiled", "linear_large")
+# The route each op forces: AUTO (w8a8_linear's own dispatch), the v_dot4
+# GEMV family at any M, and the MFMA GEMM family at any M.
+LINEAR_ROUTES = ("linear", "linear_dot4", "linear_mfma")
+# The reference's four M > 1 tensor-core entry points (src/kernels.rs:846-1289)
+# are names for the MFMA route here.
+MFMA_ALIASES = ("linear_prefill", "linear_splitk", "linear_tiled", "linear_large")
 
 
-def test_linear_fixtures_every_kernel_family(env, fixtures):
+def test_linear_fixtures_auto_dot4_and_mfma_routes(env, fixtures):
     ctx, mod, s = env
     for c in fixtures.cases("linear"):
         k = c["width"]
         q, asc, w, ws = (dev(s, fixtures.tensor(c, key)) for key in ("q", "asc", "w", "ws"))
         want = fixtures.tensor(c, "out").reshape(-1)
         want_acc = fixtures.tensor(c, "acc").reshape(-1)
-        for op in LINEAR_OPS:
+        for op in LINEAR_ROUTES:
             for dtype, expect in ((np.float32, bits(want)), (np.uint16, (bits(want) >> 16).astype(np.uint16)),
                                   (np.int32, want_acc)):
                 out = DeviceBuffer.zeroed(s, want.size, dtype)
@@ -132,6 +136,20 @@ def test_linear_fixtures_every_kernel_family(env, fixtures):
                 if dtype is np.float32:
                     got = bits(got)
                 assert np.array_equal(got, expect), f"{op} {np.dtype(dtype)} {c['name']}"
+
+
+def test_reference_tensor_core_names_take_the_mfma_route(env, fixtures):
+    """linear_prefill / _splitk / _tiled / _large keep the reference's call
+    sites working; each is the MFMA route, checked once per fixture."""
+    ctx, mod, s = env
+    for c in fixtures.cases("linear"):
+        k = c["width"]
+        q, asc, w, ws = (dev(s, fixtures.tensor(c, key)) for key in ("q", "asc", "w", "ws"))
+        want_acc = fixtures.tensor(c, "acc").reshape(-1)
+        for op in MFMA_ALIASES:
+            out = DeviceBuffer.zeroed(s, want_acc.size, np.int32)
+            getattr(mod, op)(s, None, q, asc, w, ws, k, out)
+            assert np.array_equal(out.to_host_vec(s), want_acc), f"{op} {c['name']}"
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200, 256])
@@ -193,6 +211,48 @@ def test_pair_triple_share_activations(env, fixtures):
         outs = [DeviceBuffer.zeroed(s, want.size, np.float32) for _ in range(3)]
         mod.linear_triple(s, None, q, asc, k, w, ws, outs[0], w, ws, outs[1], w, ws, outs[2])
         assert all(np.array_equal(bits(o.to_host_vec(s)), want) for o in outs)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3])
+@pytest.mark.parametrize("k,ns", [(4096, (4096, 1024, 1024)),       # qkv call site, src/gpu.rs:571-590
+                                  (4096, (33, 1000, 4099, 7)),      # count 4, unequal and ragged N
+                                  (12288, (4096, 1024)),
+                                  (1040, (517, 64, 3))])
+def test_grouped_distinct_matrices(env, m, k, ns):
+    """linear_triple (src/kernels.rs:736-806) / linear_pair / count 4 with a
+    different matrix, scale vector and N in every slot: each output equals
+    its own projection in the oracle (i32, BF16 and f32), so a slot that read
+    a neighbour's matrix, scales or row range would fail.  m = 1 runs the
+    one-launch GEMV (gemv_m1 with two rows per wave at k = 4096 here), m = 2
+    the multi-row GEMV (gemv_mt), m = 3 one MFMA launch per member."""
+    ctx, mod, s = env
+    rng = np.random.default_rng(7000 + 31 * m + len(ns) + k)
+    q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+    mats = []
+    for i, n in enumerate(ns):
+        w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        w[0, :] = 127 - i                       # a distinct first row per slot
+        ws = (rng.random(n) / 64 + 1e-4 * (i + 1)).astype(F32)
+        mats.append((w, ws))
+    dq, da = dev(s, q), dev(s, asc)
+    dmats = [(dev(s, w), dev(s, ws)) for w, ws in mats]
+    want = [oracle.linear(q, asc, w, ws, k) for w, ws in mats]
+    for dtype in (np.int32, np.uint16, np.float32):
+        outs = [DeviceBuffer.zeroed(s, m * n, dtype) for n in ns]
+        mod.linear_grouped(s, dq, da, k, [(dw, dws, o) for (dw, dws), o in zip(dmats, outs)])
+        for i, (o, (acc, out, outb)) in enumerate(zip(outs, want)):
+            got = o.to_host_vec(s)
+            exp = acc if dtype is np.int32 else outb if dtype is np.uint16 else out
+            if dtype is np.float32:
+                got, exp = bits(got), bits(exp)
+            assert np.array_equal(got, exp.reshape(-1)), f"slot {i} n={ns[i]} {np.dtype(dtype)}"
+    if len(ns) == 3:
+        outs = [DeviceBuffer.zeroed(s, m * n, np.uint16) for n in ns]
+        (w0, s0), (w1, s1), (w2, s2) = dmats
+        mod.linear_triple(s, None, dq, da, k, w0, s0, outs[0], w1, s1, outs[1], w2, s2, outs[2])
+        for i, (o, (_, _, outb)) in enumerate(zip(outs, want)):
+            assert np.array_equal(o.to_host_vec(s), outb.reshape(-1)), f"linear_triple slot {i}"
 
 
 @pytest.mark.parametrize("k,n", [(128, 33), (4096, 12288)])
@@ -371,6 +431,46 @@ def test_graph_replay_matches_eager(env):
         step()  # eager work between replays
         s.synchronize()
         assert int(tok.to_host_vec(s)[0]) == eager[2]
+
+
+def test_selection_workspace_growth_keeps_captured_graph_valid(env):
+    """A graph captured with select_token keeps its workspace address: an
+    eager linear_argmax that needs a larger selection workspace retires the
+    old buffer instead of freeing it, so every replay still writes live
+    memory and returns the right token.  Growing under capture is refused."""
+    ctx, mod0, s = env
+    mod = load(ctx)                       # fresh workspaces
+    x = (np.arange(5000) % 97).astype(F32)
+    x[617] = 4000.0
+    dx, tok = dev(s, x), DeviceBuffer.zeroed(s, 1, np.uint32)
+    mod.select_token(s, None, dx, tok)
+    s.synchronize()
+    assert int(tok.to_host_vec(s)[0]) == 617
+    g = Graph(s)
+    with g:
+        mod.select_token(s, None, dx, tok)
+    # grow: 400,000 vocabulary rows need more keys than the first buffer holds
+    n, k = 400_000, 16
+    rng = np.random.default_rng(5)
+    q = rng.integers(-127, 128, size=(1, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    asc, ws = np.array([0.01], F32), (rng.random(n) / 64 + 1e-4).astype(F32)
+    want, _ = oracle.linear_argmax(q, asc, w, ws, k)
+    before = len(mod._retired)
+    t2 = DeviceBuffer.zeroed(s, 1, np.uint32)
+    mod.linear_argmax(s, dev(s, q), dev(s, asc), dev(s, w), dev(s, ws), k, t2)
+    s.synchronize()
+    assert int(t2.to_host_vec(s)[0]) == want
+    assert len(mod._retired) == before + 1
+    for rep in range(3):
+        tok.fill_zero(s)
+        g.launch()
+        s.synchronize()
+        assert int(tok.to_host_vec(s)[0]) == 617, rep
+    mod3 = load(ctx)
+    with pytest.raises(W8A8Error):
+        with Graph(s):
+            mod3.select_token(s, None, dx, tok)
 
 
 # ------------------------------------------------------------------ synthetic
