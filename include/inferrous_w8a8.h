@@ -282,6 +282,23 @@ int w8a8_linear_argmax(void *stream, const int8_t *q, const float *asc,
                        uint32_t *token, void *logits, int logits_dtype,
                        void *workspace, size_t workspace_bytes);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): w8a8_linear_argmax with its selection keys in a fixed device
+ * array inside the library instead of a caller workspace.  Same results as
+ * w8a8_linear_argmax.  The array holds the keys of at most
+ * W8A8_NOALLOC_MAX_ROWS vocabulary rows (512 KiB on each GPU the library
+ * runs on, kept until the process ends); larger n returns W8A8_ESHAPE.
+ * Nothing is allocated and no state carries between calls (each call writes
+ * every key it reads), but every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, or two threads) race and may
+ * return a wrong token. */
+#define W8A8_NOALLOC_MAX_ROWS 262144
+int w8a8_linear_argmax_noalloc(void *stream, const int8_t *q, const float *asc,
+                               const int8_t *w, const float *ws, size_t n,
+                               uint32_t k, uint32_t *token, void *logits,
+                               int logits_dtype);
+
 /* ------------------------------------------------------------------ synthetic
  * Seeded generators for benches and tests (no reference counterpart; the
  * reference loads exported bundles, src/model.rs:46-165).  Pure functions of

@@ -14,6 +14,7 @@ OK = 0
 ENULL, ESHAPE, EALIGN, EINIT, EWORKSPACE, EARG, ENODEV = -1, -2, -3, -4, -5, -6, -7
 OUT_F32, OUT_BF16, OUT_I32 = 0, 1, 2
 PATH_AUTO, PATH_DOT4, PATH_MFMA = 0, 1, 2
+NOALLOC_MAX_ROWS = 262144  # W8A8_NOALLOC_MAX_ROWS
 
 P = ctypes.c_void_p
 S = ctypes.c_size_t
@@ -71,6 +72,7 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_select_token": (I, [P, P, S, P, P, S]),
     "w8a8_linear_argmax_workspace_bytes": (S, [S]),
     "w8a8_linear_argmax": (I, [P, P, P, P, P, S, U32, P, P, I, P, S]),
+    "w8a8_linear_argmax_noalloc": (I, [P, P, P, P, P, S, U32, P, P, I]),
     "w8a8_synth_i8": (I, [P, P, S, U64, U64]),
     "w8a8_synth_f32": (I, [P, P, S, U64, U64, F, F]),
 }

@@ -18,10 +18,19 @@
 
 using namespace w8a8;
 
+// Selection keys of w8a8_linear_argmax_noalloc: a file-scope device array,
+// one copy per GPU, held until the process ends.  In host code `scratch` is
+// only a stand-in for the symbol; w8a8_init looks up each device's own
+// address once (hipGetSymbolAddress, with that device current) and every
+// launch uses that address.
+static constexpr size_t kNoallocKeys = argmax_keys_for(W8A8_NOALLOC_MAX_ROWS);
+static __device__ __align__(256) uint64_t scratch[kNoallocKeys];
+
 namespace {
 
 std::mutex g_init_mu;
 std::atomic<uint64_t> g_ready_mask{0};  // devices that passed w8a8_init
+std::atomic<void*> g_scratch[64];  // per device: the address of `scratch` below
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? W8A8_OK : (int)e; }
 
@@ -98,6 +107,39 @@ int run_linear(hipStream_t st, const int8_t* q, const float* asc, size_t m, cons
   return hip_status(launch_gemm(st, g));
 }
 
+
+int check_argmax(const int8_t* q, const float* asc, const int8_t* w, const float* ws, size_t n,
+                 uint32_t k, const uint32_t* token, const void* logits, int logits_dtype) {
+  if (logits && logits_dtype != W8A8_OUT_F32 && logits_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  if (!token) return W8A8_ENULL;
+  if (n > 0) {
+    // validate as a 1-row projection; logits are optional
+    int s = check_linear(q, asc, 1, w, ws, n, k, logits ? logits : (const void*)token,
+                         logits ? logits_dtype : W8A8_OUT_F32);
+    if (s != W8A8_OK) return s;
+  }
+  if (!al(token, 4)) return W8A8_EALIGN;
+  return W8A8_OK;
+}
+
+int run_argmax(hipStream_t st, const int8_t* q, const float* asc, const int8_t* w, const float* ws,
+               size_t n, uint32_t k, uint32_t* token, void* logits, int logits_dtype, uint64_t* keys) {
+  GemvArgs a{};
+  a.q = q;
+  a.asc = asc;
+  a.m = 1;
+  a.k = k;
+  a.count = 1;
+  a.w[0] = w;
+  a.ws[0] = ws;
+  a.n[0] = (uint32_t)n;
+  a.out[0] = logits;
+  a.out_dtype = logits ? logits_dtype : W8A8_OUT_F32;
+  a.slots = keys;
+  a.token = token;
+  return hip_status(launch_gemv_argmax(st, a));
+}
+
 }  // namespace
 
 extern "C" {
@@ -150,6 +192,13 @@ int w8a8_init(int device) {
   // force code-object load now (device::load) rather than at first launch
   e = hipFree(nullptr);
   if (e != hipSuccess) return hip_status(e);
+  if (!g_scratch[device].load(std::memory_order_acquire)) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e);
+    if (!p) return W8A8_ENODEV;
+    g_scratch[device].store(p, std::memory_order_release);
+  }
   g_ready_mask.fetch_or(1ull << device, std::memory_order_acq_rel);
   return W8A8_OK;
 }
@@ -598,36 +647,35 @@ size_t w8a8_linear_argmax_workspace_bytes(size_t n) {
   return std::max<size_t>(1, argmax_keys_bound(n)) * sizeof(uint64_t);
 }
 
+
 int w8a8_linear_argmax(void* stream, const int8_t* q, const float* asc, const int8_t* w,
                        const float* ws, size_t n, uint32_t k, uint32_t* token, void* logits,
                        int logits_dtype, void* workspace, size_t workspace_bytes) {
-  if (logits && logits_dtype != W8A8_OUT_F32 && logits_dtype != W8A8_OUT_BF16) return W8A8_EARG;
-  if (!token) return W8A8_ENULL;
-  if (n > 0) {
-    // validate as a 1-row projection; logits are optional
-    int s = check_linear(q, asc, 1, w, ws, n, k, logits ? logits : (void*)token,
-                         logits ? logits_dtype : W8A8_OUT_F32);
-    if (s != W8A8_OK) return s;
-  }
-  if (!al(token, 4)) return W8A8_EALIGN;
+  int s = check_argmax(q, asc, w, ws, n, k, token, logits, logits_dtype);
+  if (s != W8A8_OK) return s;
   if (!workspace || workspace_bytes < w8a8_linear_argmax_workspace_bytes(n)) return W8A8_EWORKSPACE;
   if (!al(workspace, 8)) return W8A8_EALIGN;
   if (!ready()) return W8A8_EINIT;
-  GemvArgs a{};
-  a.q = q;
-  a.asc = asc;
-  a.m = 1;
-  a.k = k;
-  a.count = 1;
-  a.w[0] = w;
-  a.ws[0] = ws;
-  a.n[0] = (uint32_t)n;
-  a.out[0] = logits;
-  a.out_dtype = logits ? logits_dtype : W8A8_OUT_F32;
-  a.slots = (uint64_t*)workspace;
-  a.token = token;
-  return hip_status(launch_gemv_argmax((hipStream_t)stream, a));
+  return run_argmax((hipStream_t)stream, q, asc, w, ws, n, k, token, logits, logits_dtype,
+                    (uint64_t*)workspace);
 }
+
+int w8a8_linear_argmax_noalloc(void* stream, const int8_t* q, const float* asc, const int8_t* w,
+                               const float* ws, size_t n, uint32_t k, uint32_t* token, void* logits,
+                               int logits_dtype) {
+  if (n > W8A8_NOALLOC_MAX_ROWS) return W8A8_ESHAPE;
+  int s = check_argmax(q, asc, w, ws, n, k, token, logits, logits_dtype);
+  if (s != W8A8_OK) return s;
+  if (!ready()) return W8A8_EINIT;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return W8A8_EINIT;
+  void* keys = g_scratch[dev].load(std::memory_order_acquire);
+  if (!keys) return W8A8_EINIT;
+  static_assert(kNoallocKeys >= argmax_keys_for(W8A8_NOALLOC_MAX_ROWS), "scratch holds every key");
+  return run_argmax((hipStream_t)stream, q, asc, w, ws, n, k, token, logits, logits_dtype,
+                    static_cast<uint64_t*>(keys));
+}
+
 
 int w8a8_synth_i8(void* stream, int8_t* out, size_t n, uint64_t seed, uint64_t stream_id) {
   if (n == 0) return W8A8_OK;

@@ -485,7 +485,8 @@ hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a) {
 size_t argmax_keys_bound(size_t n) {
   // every route puts at least one row per wave and at least kGemvWaves waves
   // per workgroup
-  return (n + kGemvWaves - 1) / kGemvWaves;
+  static_assert(kGemvWaves == kArgmaxRowsPerKey, "selection key bound");
+  return argmax_keys_for(n);
 }
 
 hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {

@@ -11,6 +11,10 @@ namespace w8a8 {
 
 constexpr int kMaxGroup = 4;
 constexpr int kSelectBlocks = 1024;  // stand-alone selection: at most this many workgroups (one u64 key each)
+// The fused lm_head selection writes one u64 key per workgroup; every route
+// gives a workgroup at least this many vocabulary rows.
+constexpr size_t kArgmaxRowsPerKey = 4;
+constexpr size_t argmax_keys_for(size_t n) { return (n + kArgmaxRowsPerKey - 1) / kArgmaxRowsPerKey; }
 
 // One GEMV launch: up to kMaxGroup sibling projections sharing q/asc.
 struct GemvArgs {

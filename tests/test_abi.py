@@ -299,3 +299,16 @@ def test_module_grouped_and_swiglu_check_operand_lengths():
     with pytest.raises(ValueError, match="q"):
         mod.linear_swiglu(None, None, _fake(k, np.int8), asc, k, good, ws, out, good, ws, out, out, None)
 
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_noalloc_argmax_validation():
+    """Rows beyond the fixed key array are refused with ESHAPE before any
+    device call; the other checks are w8a8_linear_argmax's."""
+    L = _lib.lib()
+    top = _lib.NOALLOC_MAX_ROWS
+    assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, top + 1, 4096, A, None, 0) == _lib.ESHAPE
+    assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, top, 4096, A, None, 0) == _lib.EINIT
+    assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, top, 4096, None, None, 0) == _lib.ENULL
+    assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, top, 4096, A + 2, None, 0) == _lib.EALIGN
+    assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, top, 4096, A, A, 7) == _lib.EARG
+    assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, 33, 4004, A, None, 0) == _lib.ESHAPE
