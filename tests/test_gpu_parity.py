@@ -502,7 +502,8 @@ def test_errors_raise_not_fall_back(env):
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     """w8a8_linear_ex with a workspace (split-K partials + exact i32 epilogue)
-    equals the call without one and the oracle, bit for bit."""
+    equals the call without one and the oracle, bit for bit -- also on a
+    second call with the same workspace, which carries nothing between calls."""
     from inferrous_amd import _lib
     ctx, mod, s = env
     print(f"split-K m={m} n={n} k={k} {np.dtype(dtype).name} res={res}", flush=True)
@@ -521,7 +522,7 @@ def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     work = DeviceBuffer.zeroed(s, need, np.uint8)
     dt = {np.float32: _lib.OUT_F32, np.uint16: _lib.OUT_BF16, np.int32: _lib.OUT_I32}[dtype]
     outs = []
-    for wp, wb in ((work.ptr, need), (None, 0), (work.ptr, need - 1)):
+    for wp, wb in ((work.ptr, need), (None, 0), (work.ptr, need - 1), (work.ptr, need)):
         out = DeviceBuffer.zeroed(s, m * n, dtype)
         comb = DeviceBuffer.zeroed(s, m * n, dtype) if res else None
         _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k,
@@ -542,6 +543,33 @@ def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
         assert np.array_equal(outs[0][1], want)
     else:
         assert np.array_equal(bits(got), bits(of))
+
+
+def test_split_k_workspace_shared_by_shapes(env):
+    """One workspace used by split-K launches of different shapes in turn
+    (different slab counts and sizes, each call overwriting what the last
+    left): every call is bit-exact against the oracle."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    lib = _lib.lib()
+    shapes = [(129, 4096, 12288), (512, 4096, 12288), (129, 6144, 4096), (40, 6144, 4096), (129, 4096, 12288),
+              (255, 1024, 4096), (512, 4096, 12288)]
+    need = max(lib.w8a8_linear_workspace_bytes(m, n, k) for m, n, k in shapes)
+    work = DeviceBuffer.zeroed(s, need, np.uint8)
+    for i, (m, n, k) in enumerate(shapes):
+        print(f"shared workspace call {i}: m={m} n={n} k={k}", flush=True)
+        assert lib.w8a8_linear_workspace_bytes(m, n, k) > 0
+        rng = np.random.default_rng(i * 101 + m)
+        q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+        w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+        ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+        dq, da, dw, dws = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws)
+        out = DeviceBuffer.zeroed(s, m * n, np.uint16)
+        _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k, None, out.ptr, None,
+                                      _lib.OUT_BF16, _lib.PATH_AUTO, work.ptr, need))
+        _, _, ob = oracle.linear(q, asc, w, ws, k, threads=8)
+        assert np.array_equal(out.to_host_vec(s), ob), f"call {i}"
 
 
 def test_large_row_counts_beyond_grid_y(env):
