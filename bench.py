@@ -435,7 +435,7 @@ def main() -> int:
                            DeviceBuffer.view_of(gw, ffn * 4096, ffn * 4096),
                            DeviceBuffer.view_of(gws, ffn, ffn)))
 
-        def layer_chain():
+        def layer_chain(fused_mlp: bool = False):
             for mats, (wg_, sg_, wu_, su_) in zip(layers, halves):
                 (_, _, _, wqkv, sqkv), (_, _, _, wo, so), _, (_, _, _, wd, sd) = mats
                 mod.norm_quantize(s, None, xs[4096], gains[0], normed, q4, sc4, mx)
@@ -443,20 +443,36 @@ def main() -> int:
                 mod.quantize(s, None, xs[4096], 4096, q4, sc4)
                 mod.linear_residual(s, None, q4, sc4, wo, so, 4096, resid, outs["o"], comb)
                 mod.norm_quantize(s, None, xs[4096], gains[1], normed, q4, sc4, mx)
-                mod.linear_swiglu(s, None, q4, sc4, 4096, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx)
-                mod.linear_quantize_with_max(s, None, act, ffn, mx, q12, sc12, wd, sd, outs["down"],
-                                             resid, comb)
+                if fused_mlp:
+                    mod.linear_swiglu_quantize(s, None, q4, sc4, 4096, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx,
+                                               q12, sc12)
+                    mod.linear_residual(s, None, q12, sc12, wd, sd, ffn, resid, outs["down"], comb)
+                else:
+                    mod.linear_swiglu(s, None, q4, sc4, 4096, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx)
+                    mod.linear_quantize_with_max(s, None, act, ffn, mx, q12, sc12, wd, sd, outs["down"],
+                                                 resid, comb)
             mod.quantize(s, None, xs[hk], hk, q4, sc4)
             mod.linear_argmax(s, q4, sc4, head_w, head_s, hk, token)
 
         layer_chain()
         s.synchronize()
         ms = time_graph(capture(layer_chain), 20)
+        # launches per layer: norm_quantize, qkv, quantize, o, norm_quantize,
+        # swiglu GEMV + its row-maximum workgroup, quantize_with_max, down
         extras["decode_reference_chain"] = {
             "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-            "launches": 8 * synth.LAYERS + 3,
+            "launches": 9 * synth.LAYERS + 3,
             "chain": "norm_quantize, qkv, quantize, o+residual, norm_quantize, linear_swiglu, quantize_with_max, down+residual; lm_head"}
         log(f"reference decode chain: {ms * 1e3:.1f} us ({extras['decode_reference_chain']['GB/s']} GB/s)")
+        # the same chain with the MLP pair linear_swiglu + quantize_with_max
+        # as one linear_swiglu_quantize call (its row tail folds the maximum
+        # and quantizes the down input in one workgroup)
+        ms = time_graph(capture(lambda: layer_chain(fused_mlp=True)), 20)
+        extras["decode_chain_fused_mlp"] = {
+            "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "launches": 8 * synth.LAYERS + 3,
+            "chain": "norm_quantize, qkv, quantize, o+residual, norm_quantize, linear_swiglu_quantize, down+residual; lm_head"}
+        log(f"decode chain, fused MLP tail: {ms * 1e3:.1f} us ({extras['decode_chain_fused_mlp']['GB/s']} GB/s)")
         # latency-bound producers at M = 1: per call in a graph of 100
         # stream-ordered calls (launch gap included)
         act12 = DeviceBuffer.from_host(s, synth.normal_rows(45, 1, ffn).reshape(-1))

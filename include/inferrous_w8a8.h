@@ -255,6 +255,22 @@ int w8a8_linear_swiglu(void *stream, const int8_t *q, const float *asc,
                        const float *ws_up, size_t n, void *gate, void *up,
                        void *act, uint32_t *maxima, int out_dtype);
 
+/* The decode MLP's linear_swiglu (src/gpu.rs:730) followed by the
+ * quantize_with_max of its act (src/gpu.rs:381, src/kernels.rs:453-475) in
+ * one call: gate, up, act and maxima exactly as w8a8_linear_swiglu, then
+ * q_out [m, n] int8 and scales_out [m] exactly as w8a8_quantize_with_max
+ * writes them from act and the folded maxima.  maxima is required (the
+ * caller resets it beforehand, as for w8a8_linear_swiglu).  At m = 1 it is
+ * two launches (the GEMV, then one workgroup that folds the maximum and
+ * quantizes the row); the separate calls take three. */
+int w8a8_linear_swiglu_quantize(void *stream, const int8_t *q, const float *asc,
+                                size_t m, uint32_t k, const int8_t *w_gate,
+                                const float *ws_gate, const int8_t *w_up,
+                                const float *ws_up, size_t n, void *gate,
+                                void *up, void *act, uint32_t *maxima,
+                                int8_t *q_out, float *scales_out,
+                                int out_dtype);
+
 /* `swiglu` (src/kernels.rs:2172-2190): act = as above, elementwise over
  * gate/up [rows, width] in dtype (F32 or BF16); maxima as above, per row
  * (the reference publishes only for its single 12288-wide decode row). */

@@ -67,6 +67,7 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_linear_ex": (I, [P, P, P, S, P, P, S, U32, P, P, P, I, I, P, S]),
     "w8a8_linear_quantize_with_max": (I, [P, P, P, S, U32, P, P, P, P, S, P, P, P, I]),
     "w8a8_linear_swiglu": (I, [P, P, P, S, U32, P, P, P, P, S, P, P, P, P, I]),
+    "w8a8_linear_swiglu_quantize": (I, [P, P, P, S, U32, P, P, P, P, S, P, P, P, P, P, P, I]),
     "w8a8_swiglu": (I, [P, P, P, S, U32, P, P, I]),
     "w8a8_select_workspace_bytes": (S, [S]),
     "w8a8_select_token": (I, [P, P, S, P, P, S]),

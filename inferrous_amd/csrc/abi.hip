@@ -587,10 +587,12 @@ int w8a8_swiglu(void* stream, const void* gate, const void* up, size_t rows, uin
   return hip_status(launch_swiglu((hipStream_t)stream, gate, up, rows, width, act, dtype, maxima));
 }
 
-int w8a8_linear_swiglu(void* stream, const int8_t* q, const float* asc, size_t m, uint32_t k,
-                       const int8_t* w_gate, const float* ws_gate, const int8_t* w_up,
-                       const float* ws_up, size_t n, void* gate, void* up, void* act,
-                       uint32_t* maxima, int out_dtype) {
+// linear_swiglu, and with q_out the quantize_with_max of its act that the
+// decode chain runs next (src/gpu.rs:377-390).
+static int run_swiglu(void* stream, const int8_t* q, const float* asc, size_t m, uint32_t k,
+                      const int8_t* w_gate, const float* ws_gate, const int8_t* w_up, const float* ws_up, size_t n,
+                      void* gate, void* up, void* act, uint32_t* maxima, int8_t* q_out, float* scales_out,
+                      int out_dtype) {
   if (out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
   int s = check_linear(q, asc, m, w_gate, ws_gate, n, k, gate, out_dtype);
   if (s != W8A8_OK) return s;
@@ -598,7 +600,9 @@ int w8a8_linear_swiglu(void* stream, const int8_t* q, const float* asc, size_t m
   if (s != W8A8_OK) return s;
   if (m == 0 || n == 0) return W8A8_OK;
   if (!act) return W8A8_ENULL;
-  if (!al(act, out_align(out_dtype)) || !al(maxima, 4)) return W8A8_EALIGN;
+  if (q_out && (!maxima || !scales_out)) return W8A8_ENULL;
+  if (n > 0xffffffffu) return W8A8_ESHAPE;
+  if (!al(act, out_align(out_dtype)) || !al(maxima, 4) || !al(scales_out, 4)) return W8A8_EALIGN;
   if (!ready()) return W8A8_EINIT;
   hipStream_t st = (hipStream_t)stream;
   if (m == 1 && (k == 4096 || k == 12288)) {
@@ -616,6 +620,8 @@ int w8a8_linear_swiglu(void* stream, const int8_t* q, const float* asc, size_t m
     a.act = act;
     a.out_dtype = out_dtype;
     a.maxima = maxima;
+    a.q_out = q_out;
+    a.scales_out = scales_out;
     return hip_status(launch_gemv_swiglu(st, a));
   }
   const int8_t* w[2] = {w_gate, w_up};
@@ -624,7 +630,26 @@ int w8a8_linear_swiglu(void* stream, const int8_t* q, const float* asc, size_t m
   void* out[2] = {gate, up};
   s = w8a8_linear_grouped(stream, q, asc, m, k, 2, w, ws, nn, out, out_dtype);
   if (s != W8A8_OK) return s;
-  return hip_status(launch_swiglu(st, gate, up, m, (uint32_t)n, act, out_dtype, maxima));
+  s = hip_status(launch_swiglu(st, gate, up, m, (uint32_t)n, act, out_dtype, maxima));
+  if (s != W8A8_OK || !q_out) return s;
+  return hip_status(launch_swiglu_quantize_rows(st, act, m, (uint32_t)n, out_dtype, maxima, q_out, scales_out));
+}
+
+int w8a8_linear_swiglu(void* stream, const int8_t* q, const float* asc, size_t m, uint32_t k,
+                       const int8_t* w_gate, const float* ws_gate, const int8_t* w_up,
+                       const float* ws_up, size_t n, void* gate, void* up, void* act,
+                       uint32_t* maxima, int out_dtype) {
+  return run_swiglu(stream, q, asc, m, k, w_gate, ws_gate, w_up, ws_up, n, gate, up, act, maxima, nullptr,
+                    nullptr, out_dtype);
+}
+
+int w8a8_linear_swiglu_quantize(void* stream, const int8_t* q, const float* asc, size_t m, uint32_t k,
+                                const int8_t* w_gate, const float* ws_gate, const int8_t* w_up,
+                                const float* ws_up, size_t n, void* gate, void* up, void* act,
+                                uint32_t* maxima, int8_t* q_out, float* scales_out, int out_dtype) {
+  if (!maxima || !q_out || !scales_out) return W8A8_ENULL;
+  return run_swiglu(stream, q, asc, m, k, w_gate, ws_gate, w_up, ws_up, n, gate, up, act, maxima, q_out,
+                    scales_out, out_dtype);
 }
 
 size_t w8a8_select_workspace_bytes(size_t n) {

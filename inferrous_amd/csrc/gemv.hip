@@ -346,33 +346,72 @@ __device__ __forceinline__ float load_val(const void* p, size_t i, int dtype) {
   return reinterpret_cast<const float*>(p)[i];
 }
 
-// Producer half of the maxima protocol for the fused M = 1 SwiGLU GEMV: the
-// row's largest bits(|act|) (NaN -> 0) folded into *maxima with a single
-// atomicMax, by one workgroup reading the act row the GEMV wrote (every
-// load of a round is issued before the first compare; indices clamped).
-// Publishing from each of the GEMV's 3,072 workgroups instead, right after
-// the maximum was reset to its floor, made most of them atomics on the same
-// word: 32.2 us per gate/up GEMV against 16.5 us without.
-constexpr int kRowMaxThreads = 1024;
+// SwiGLU row tail, one workgroup per act row (blockIdx.x).  FOLD: the row's
+// largest bits(|act|) (NaN -> 0) is folded into maxima[row] with one
+// atomicMax -- the producer half of the quantize_with_max protocol
+// (src/kernels.rs:133-147) for the fused M = 1 GEMV, which publishes
+// nothing itself.  Publishing from each of that GEMV's 3,072 workgroups
+// instead, right after the maximum was reset to its floor, made most of them
+// atomics on the same word: 32.2 us per gate/up GEMV against 16.5 us
+// without.  With q != null the row is then quantized exactly as
+// quantize_with_max (src/kernels.rs:453-475) does with the folded maximum:
+// s = RN(from_bits(maxima[row]) / 127), q_j = round(RN(act_j / s)).  A row
+// of up to 16,384 values is loaded once, all loads issued before the first
+// use (indices clamped), and kept in registers for both passes.
+constexpr int kRowTailThreads = 1024;
+constexpr int kRowTailCache = 16;  // act values per thread held in registers (rows up to 16,384 wide)
 
-__global__ __launch_bounds__(kRowMaxThreads) void row_absmax_kernel(const void* act, uint32_t n, int dtype,
-                                                                     uint32_t* maxima) {
-  __shared__ uint32_t wmax[kRowMaxThreads / 64];
-  uint32_t bits = 0;
-  for (uint32_t base = 0; base < n; base += kRowMaxThreads * 4) {
-    float v[4];
+template <bool FOLD>
+__global__ __launch_bounds__(kRowTailThreads) void swiglu_row_tail(const void* act, uint32_t n, int dtype,
+                                                                    uint32_t* maxima, int8_t* q, float* scales) {
+  __shared__ uint32_t wmax[kRowTailThreads / 64];
+  __shared__ uint32_t row_max;
+  const size_t r = blockIdx.x, base_i = r * (size_t)n;
+  // Only this workgroup folds into maxima[r] during the call, so the value
+  // before the fold can be read up front, and the fold needs no return.
+  uint32_t before = 0;
+  if (threadIdx.x == 0) before = maxima[r];
+  const bool cached = n <= (uint32_t)(kRowTailThreads * kRowTailCache);
+  float v[kRowTailCache];
+  if (cached) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = load_val(act, min(base + u * kRowMaxThreads + threadIdx.x, n - 1), dtype);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) bits = max(bits, abs_bits_no_nan(v[u]));
+    for (int u = 0; u < kRowTailCache; ++u)
+      v[u] = load_val(act, base_i + min(u * kRowTailThreads + threadIdx.x, n - 1), dtype);
   }
-  bits = wave_max_u32(bits);
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = bits;
-  __syncthreads();
-  if (threadIdx.x == 0) {
+  if (FOLD) {
+    uint32_t bits = 0;
+    if (cached) {
 #pragma unroll
-    for (int i = 0; i < kRowMaxThreads / 64; ++i) bits = max(bits, wmax[i]);
-    atomicMax(maxima, bits);
+      for (int u = 0; u < kRowTailCache; ++u) bits = max(bits, abs_bits_no_nan(v[u]));
+    } else {
+      for (uint32_t j = threadIdx.x; j < n; j += kRowTailThreads)
+        bits = max(bits, abs_bits_no_nan(load_val(act, base_i + j, dtype)));
+    }
+    bits = wave_max_u32(bits);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = bits;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int i = 0; i < kRowTailThreads / 64; ++i) bits = max(bits, wmax[i]);
+      atomicMax(maxima + r, bits);
+      row_max = max(before, bits);
+    }
+  } else if (threadIdx.x == 0) {
+    row_max = before;
+  }
+  if (!q) return;
+  __syncthreads();
+  const float s = __uint_as_float(row_max) / 127.0f;
+  if (threadIdx.x == 0) scales[r] = s;
+  if (cached) {
+#pragma unroll
+    for (int u = 0; u < kRowTailCache; ++u) {
+      const uint32_t j = u * kRowTailThreads + threadIdx.x;
+      if (j < n) q[base_i + j] = round_i8(v[u] / s);
+    }
+  } else {
+    for (uint32_t j = threadIdx.x; j < n; j += kRowTailThreads)
+      q[base_i + j] = round_i8(load_val(act, base_i + j, dtype) / s);
   }
 }
 
@@ -527,7 +566,17 @@ hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !a.maxima) return e;
-  hipLaunchKernelGGL(row_absmax_kernel, dim3(1), dim3(kRowMaxThreads), 0, st, a.act, a.n, a.out_dtype, a.maxima);
+  hipLaunchKernelGGL(swiglu_row_tail<true>, dim3(1), dim3(kRowTailThreads), 0, st, a.act, a.n, a.out_dtype,
+                     a.maxima, a.q_out, a.scales_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_quantize_rows(hipStream_t st, const void* act, size_t rows, uint32_t width, int dtype,
+                                       const uint32_t* maxima, int8_t* q, float* scales) {
+  if (rows == 0 || width == 0) return hipSuccess;
+  if (rows > 0x7fffffffu) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(swiglu_row_tail<false>, dim3((unsigned)rows), dim3(kRowTailThreads), 0, st, act, width, dtype,
+                     const_cast<uint32_t*>(maxima), q, scales);
   return hipGetLastError();
 }
 

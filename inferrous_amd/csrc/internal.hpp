@@ -48,6 +48,8 @@ struct SwigluArgs {
   void* act;
   int out_dtype;      // F32 or BF16
   uint32_t* maxima;   // optional: atomicMax of bits(|act|)
+  int8_t* q_out;      // optional (with maxima): act quantized with the folded maximum
+  float* scales_out;
 };
 
 struct GemmArgs {
@@ -88,6 +90,9 @@ hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a);  // m == 1, k in {4096, 12288}
 hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_t rows,
                          uint32_t width, void* act, int dtype, uint32_t* maxima);
+// act rows quantized as quantize_with_max does with maxima (F32 or BF16 act)
+hipError_t launch_swiglu_quantize_rows(hipStream_t st, const void* act, size_t rows, uint32_t width, int dtype,
+                                       const uint32_t* maxima, int8_t* q, float* scales);
 hipError_t launch_select(hipStream_t st, const float* x, size_t n, uint64_t* keys, uint32_t* token);
 // u64 keys the fused selection of an n-row lm_head writes (an upper bound)
 size_t argmax_keys_bound(size_t n);

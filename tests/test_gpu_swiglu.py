@@ -327,3 +327,52 @@ def test_decode_mlp_chain_combined_down_entry(env):
         s.synchronize()
         for k in names:
             assert np.array_equal(fus[k].to_host_vec(s).view(np.uint8), want[k]), f"replay {rep}: {k}"
+
+
+@pytest.mark.parametrize("m,k,n,dtype", [(1, 4096, 12288, np.float32), (1, 4096, 12288, np.uint16),
+                                         (1, 12288, 1000, np.float32), (1, 128, 33, np.uint16),
+                                         (3, 4096, 4099, np.float32), (2, 1024, 5000, np.uint16)])
+def test_linear_swiglu_quantize_matches_separate_calls(env, m, k, n, dtype):
+    """w8a8_linear_swiglu_quantize (the decode pair src/gpu.rs:730 + :381 in
+    one call) writes the same gate / up / act / maxima bits as
+    w8a8_linear_swiglu, and q_out / scales_out equal quantize_with_max of
+    act with the folded maxima (the oracle restatement of
+    src/kernels.rs:453-475) -- at M = 1 on the fused GEMV (one workgroup
+    folds the maximum and quantizes), and on the grouped / MFMA route.
+    The maxima start at a reset floor on one row and at a large stale value
+    on another, so the fold (not the row maximum) sets the scale."""
+    ctx, mod, s = env
+    print(f"linear_swiglu_quantize m={m} k={k} n={n} dtype={np.dtype(dtype).name}", flush=True)
+    rng = np.random.default_rng(m * 1009 + k + n)
+    q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    asc = (rng.random(m) / 512 + 1e-4).astype(F32)
+    w0 = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    w1 = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    s0 = (rng.random(n) / 256 + 1e-4).astype(F32)
+    s1 = (rng.random(n) / 256 + 1e-4).astype(F32)
+    start = np.full(m, FLOOR, np.uint32)
+    if m > 1:
+        start[-1] = int(np.array([1e4], F32).view(np.uint32)[0])   # larger than any |act| here
+    dq, da, dw0, dw1, ds0, ds1 = dev(s, q), dev(s, asc), dev(s, w0), dev(s, w1), dev(s, s0), dev(s, s1)
+    outs = []
+    for fused in (False, True):
+        g, u, act = (DeviceBuffer.zeroed(s, m * n, dtype) for _ in range(3))
+        maxima = dev(s, start)
+        q_out = DeviceBuffer.zeroed(s, m * n, np.int8)
+        sc_out = DeviceBuffer.zeroed(s, m, np.float32)
+        if fused:
+            mod.linear_swiglu_quantize(s, None, dq, da, k, dw0, ds0, g, dw1, ds1, u, act, maxima, q_out, sc_out)
+        else:
+            mod.linear_swiglu(s, None, dq, da, k, dw0, ds0, g, dw1, ds1, u, act, maxima)
+        outs.append({name: b.to_host_vec(s).copy() for name, b in
+                     (("g", g), ("u", u), ("act", act), ("max", maxima), ("q", q_out), ("sc", sc_out))})
+    for name in ("g", "u", "act", "max"):
+        assert np.array_equal(outs[1][name].view(np.uint8), outs[0][name].view(np.uint8)), name
+    act_v = outs[1]["act"]
+    if dtype == np.uint16:
+        act_v = (act_v.astype(np.uint32) << 16).view(F32)
+    want_q, want_s = oracle.quantize_with_max(act_v, n, outs[1]["max"])
+    assert np.array_equal(outs[1]["q"], want_q)
+    assert np.array_equal(bits(outs[1]["sc"]), bits(want_s))
+    for r in range(m):
+        assert int(outs[1]["max"][r]) == max(int(start[r]), fold_max(act_v.reshape(m, n)[r])), f"row {r}"
