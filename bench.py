@@ -576,42 +576,75 @@ def main() -> int:
 
 
 def cpu_baseline() -> dict:
-    """The C oracle (quantize + exact integer GEMV + epilogue, OpenMP over
-    output channels) timed on this host over a bounded sample of the decode
-    workload: layer 0's four projections (193 MB of int8 weights)."""
+    """The C oracle (quantize + exact integer GEMV/GEMM + epilogue, OpenMP
+    over output channels; argmax for the head) timed on this host on every
+    BASELINE config, each at all host cores (at most 16), 8 threads (the
+    reference fixture's setting, tools/operator_fixtures.py:17) and 1 thread.
+    Samples: C1 one 4096x4096 projection; C2 layer 0's four projections;
+    C3 the whole 151,936-row head with argmax; C4 the o shape (4096x4096) at
+    M = 129 and 512 on Student-t rows; C5 the down shape (4096x12288) at
+    M = 4, 16 and 64 on per-row-seeded rows.  `value` is C2 at all cores."""
     import oracle
     from inferrous_amd import synth
 
     t0 = time.time()
     nthreads = max(1, min(os.cpu_count() or 1, 16))
-    mats = []
-    for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
-        w = oracle.synth_i8(SEED_W, synth.weight_stream(0, si), 0, n * k)
-        ws = oracle.synth_f32(SEED_S, synth.scale_stream(0, si), 0, n, 1e-3, 1e-2)
-        mats.append((n, k, w, ws))
+    thread_counts = sorted({nthreads, 8, 1}, reverse=True)
+
+    def weights(layer: int, si: int):
+        _, n, k = synth.DECODE_SHAPES[si]
+        return (oracle.synth_i8(SEED_W, synth.weight_stream(layer, si), 0, n * k),
+                oracle.synth_f32(SEED_S, synth.scale_stream(layer, si), 0, n, 1e-3, 1e-2))
+
+    mats = [(n, k) + weights(0, si) for si, (_, n, k) in enumerate(synth.DECODE_SHAPES)]
     xs = {4096: synth.normal_rows(40, 1, 4096).reshape(-1), 12288: synth.normal_rows(41, 1, 12288).reshape(-1)}
-    sample_bytes = sum(gemv_bytes(n, k) for (n, k, _, _) in mats)
-    sample_ops = sum(2 * n * k for (n, k, _, _) in mats)
+    hn, hk = synth.VOCAB, synth.HIDDEN
+    hw = oracle.synth_i8(SEED_W, 9001, 0, hn * hk)
+    hs = oracle.synth_f32(SEED_S, 9101, 0, hn, 1e-3, 1e-2)
+    xh = synth.normal_rows(42, 1, hk).reshape(-1)
+    (_, _, wo, so), (_, _, wd, sd) = mats[1], mats[3]
     log(f"cpu baseline: host weights ready in {time.time() - t0:.1f}s")
 
-    def one_pass(threads: int) -> float:
-        t = time.perf_counter()
-        for (n, k, w, ws) in mats:
-            q, sc = oracle.quantize(xs[k], k)
-            oracle.linear(q, sc, w, ws, k, threads=threads)
-        return time.perf_counter() - t
+    def linear_pass(x, m, n, k, w, ws, threads):
+        q, sc = oracle.quantize(x, k)
+        oracle.linear(q, sc, w, ws, k, threads=threads)
 
-    res, gops = {}, {}
-    for threads in sorted({nthreads, 8, 1}, reverse=True):
-        one_pass(threads)
+    # (name, algorithmic bytes, integer ops 2*M*N*K, pass at `threads`)
+    configs = [("C1 linear M=1 4096x4096", gemv_bytes(4096, 4096), 2 * 4096 * 4096,
+                lambda th: linear_pass(xs[4096], 1, 4096, 4096, wo, so, th)),
+               ("C2 decode layer 0: qkv, o, gate_up, down at M=1",
+                sum(gemv_bytes(n, k) for (n, k, _, _) in mats), sum(2 * n * k for (n, k, _, _) in mats),
+                lambda th: [linear_pass(xs[k], 1, n, k, w, ws, th) for (n, k, w, ws) in mats]),
+               ("C3 lm_head 151936x4096 + argmax, M=1", gemv_bytes(hn, hk, out_bytes=0) + 4, 2 * hn * hk,
+                lambda th: oracle.linear_argmax(*oracle.quantize(xh, hk), hw, hs, hk, threads=th))]
+    for m in (129, 512):
+        x = synth.student_t_rows(700, m, 4096).reshape(-1)
+        configs.append((f"C4 prefill o 4096x4096 at M={m}", gemv_bytes(4096, 4096, m), 2 * m * 4096 * 4096,
+                        lambda th, x=x, m=m: linear_pass(x, m, 4096, 4096, wo, so, th)))
+    for m in (4, 16, 64):
+        x = synth.ragged_rows(range(9000 + 100 * m, 9000 + 100 * m + m), 12288).reshape(-1)
+        configs.append((f"C5 ragged down 4096x12288 at M={m}", gemv_bytes(4096, 12288, m), 2 * m * 4096 * 12288,
+                        lambda th, x=x, m=m: linear_pass(x, m, 4096, 12288, wd, sd, th)))
+
+    def median_seconds(fn) -> float:
+        fn()
         times = []
-        budget = time.perf_counter()
-        while len(times) < 5 or (time.perf_counter() - budget < 3.0 and len(times) < 50):
-            times.append(one_pass(threads))
-        med = float(np.median(times))
-        res[threads] = sample_bytes / med / 1e9
-        gops[threads] = sample_ops / med / 1e9
-        log(f"cpu baseline {threads} threads: {med * 1e3:.1f} ms/pass, {res[threads]:.2f} GB/s")
+        start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - start < 0.6 and len(times) < 9):
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+        return float(np.median(times))
+
+    per = {}
+    for name, nbytes, ops, fn in configs:
+        gbs, gops = {}, {}
+        for th in thread_counts:
+            sec = median_seconds(lambda: fn(th))
+            gbs[str(th)] = round(nbytes / sec / 1e9, 3)
+            gops[str(th)] = round(ops / sec / 1e9, 3)
+        per[name] = {"GB/s_by_threads": gbs, "GOPS_by_threads": gops}
+        log(f"cpu baseline {name}: GB/s {gbs}, GOPS {gops}")
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -620,13 +653,14 @@ def cpu_baseline() -> dict:
                 break
     except OSError:
         pass
-    return {"value": round(res[nthreads], 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-            "sample": (f"C oracle (quantize + int32 GEMV + BF16 epilogue) over layer 0's qkv/o/"
-                       f"gate_up/down at M=1 ({sample_bytes / 1e6:.1f} MB per pass), median of >=5 "
-                       f"passes; {cpu_model}, {os.cpu_count()} logical CPUs; GB/s at 8 threads "
-                       f"{res.get(8, 0):.3f}, at 1 thread {res.get(1, 0):.3f}"),
-            "gbs_by_threads": {str(t): round(v, 3) for t, v in res.items()},
-            "gops_by_threads": {str(t): round(v, 3) for t, v in gops.items()}}
+    c2 = per["C2 decode layer 0: qkv, o, gate_up, down at M=1"]["GB/s_by_threads"]
+    return {"value": c2[str(nthreads)], "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "sample": (f"C oracle (quantize + int32 GEMV/GEMM + BF16 epilogue; argmax for C3), median of >=3 "
+                       f"runs per point; value = C2 (layer 0's four decode projections at M=1, "
+                       f"{sum(gemv_bytes(n, k) for (n, k, _, _) in mats) / 1e6:.1f} MB) at {nthreads} threads; "
+                       f"{cpu_model}, {os.cpu_count()} logical CPUs"),
+            "cpu_model": cpu_model, "logical_cpus": os.cpu_count(),
+            "per_config": per}
 
 
 if __name__ == "__main__":
