@@ -208,6 +208,69 @@ def ragged_profile_run() -> int:
     return 0
 
 
+def chain_profile_run() -> int:
+    """Workload for a kernel-trace profile of the decode layer chain
+    (src/gpu.rs:571-790 order) at M = 1: 8 layers of distinct weights, the
+    reference call sequence and the chain with linear_swiglu_quantize, each
+    captured once and replayed 5 times."""
+    from inferrous_amd import CudaContext, DeviceBuffer, Graph, load, synth
+    ctx = CudaContext(0)
+    mod = load(ctx)
+    s = ctx.new_stream()
+    nl, ffn, h = 8, 12288, 4096
+    layers = []
+    for layer in range(nl):
+        mats = []
+        for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
+            w = DeviceBuffer.zeroed(s, n * k, np.int8)
+            ws = DeviceBuffer.zeroed(s, n, np.float32)
+            mod.synth_i8(s, w, SEED_W, synth.weight_stream(layer, si))
+            mod.synth_f32(s, ws, SEED_S, synth.scale_stream(layer, si), 1e-3, 1e-2)
+            mats.append((w, ws))
+        (gw, gws) = mats[2]
+        halves = (DeviceBuffer.view_of(gw, 0, ffn * h), DeviceBuffer.view_of(gws, 0, ffn),
+                  DeviceBuffer.view_of(gw, ffn * h, ffn * h), DeviceBuffer.view_of(gws, ffn, ffn))
+        layers.append((mats, halves))
+    x = DeviceBuffer.from_host(s, synth.normal_rows(40, 1, h).reshape(-1))
+    resid = DeviceBuffer.from_host(s, synth.normal_rows(43, 1, h).reshape(-1))
+    gains = [DeviceBuffer.from_host(s, (1 + 0.1 * synth.normal_rows(44 + i, 1, h)).astype(np.float32).reshape(-1))
+             for i in range(2)]
+    normed = DeviceBuffer.zeroed(s, h, np.float32)
+    q4, sc4 = DeviceBuffer.zeroed(s, h, np.int8), DeviceBuffer.zeroed(s, 1, np.float32)
+    q12, sc12 = DeviceBuffer.zeroed(s, ffn, np.int8), DeviceBuffer.zeroed(s, 1, np.float32)
+    mx = DeviceBuffer.zeroed(s, 1, np.uint32)
+    gbuf, ubuf, act = (DeviceBuffer.zeroed(s, ffn, np.float32) for _ in range(3))
+    qkv, o, down = (DeviceBuffer.zeroed(s, n, np.uint16) for n in (6144, h, h))
+    comb = DeviceBuffer.zeroed(s, h, np.uint16)
+
+    def chain(fused: bool):
+        for (mats, (wg_, sg_, wu_, su_)) in layers:
+            (wqkv, sqkv), (wo, so), _, (wd, sd) = mats
+            mod.norm_quantize(s, None, x, gains[0], normed, q4, sc4, mx)
+            mod.linear(s, None, q4, sc4, wqkv, sqkv, h, qkv)
+            mod.quantize(s, None, x, h, q4, sc4)
+            mod.linear_residual(s, None, q4, sc4, wo, so, h, resid, o, comb)
+            mod.norm_quantize(s, None, x, gains[1], normed, q4, sc4, mx)
+            if fused:
+                mod.linear_swiglu_quantize(s, None, q4, sc4, h, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx, q12, sc12)
+                mod.linear_residual(s, None, q12, sc12, wd, sd, ffn, resid, down, comb)
+            else:
+                mod.linear_swiglu(s, None, q4, sc4, h, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx)
+                mod.linear_quantize_with_max(s, None, act, ffn, mx, q12, sc12, wd, sd, down, resid, comb)
+
+    for fused in (False, True):
+        chain(fused)
+        s.synchronize()
+        g = Graph(s)
+        with g:
+            chain(fused)
+        for _ in range(5):
+            g.launch()
+        s.synchronize()
+        print(f"chain profile ({'fused MLP tail' if fused else 'reference calls'}) done", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,6 +284,8 @@ def main() -> int:
                     help="run only the prefill GEMM workload for a kernel-trace profile")
     ap.add_argument("--head-profile", action="store_true",
                     help="run only the packed BF16 head workload for a kernel-trace profile")
+    ap.add_argument("--chain-profile", action="store_true",
+                    help="run only the decode layer chain workload for a kernel-trace profile")
     ap.add_argument("--ragged-profile", action="store_true",
                     help="run only the ragged small-batch workload for a kernel-trace profile")
     args = ap.parse_args()
@@ -238,6 +303,8 @@ def main() -> int:
         return head_profile_run()
     if args.ragged_profile:
         return ragged_profile_run()
+    if args.chain_profile:
+        return chain_profile_run()
 
     from inferrous_amd import CudaContext, DeviceBuffer, Event, Graph, load, synth
 
