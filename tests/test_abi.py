@@ -172,6 +172,18 @@ def test_fused_and_workspace_entries_validation():
     assert sw(act=A + 2) == _lib.EALIGN
     assert sw(maxima=A + 1) == _lib.EALIGN
     assert sw(m=0) == _lib.OK and sw(n=0) == _lib.OK
+    # linear_swiglu_quantize: linear_swiglu's arguments, then maxima, q_out, scales_out (all required)
+    swq = lambda **kw: L.w8a8_linear_swiglu_quantize(  # noqa: E731
+        None, A, A, kw.get("m", 1), kw.get("k", 4096), A, A, A, A, 12288, A, A, kw.get("act", A),
+        kw.get("maxima", A), kw.get("qo", A), kw.get("so", A), kw.get("dtype", F32))
+    assert swq() == _lib.EINIT
+    assert swq(maxima=None) == _lib.ENULL
+    assert swq(qo=None) == _lib.ENULL and swq(so=None) == _lib.ENULL
+    assert swq(dtype=I32) == _lib.EARG
+    assert swq(k=4095) == _lib.ESHAPE
+    assert swq(so=A + 2) == _lib.EALIGN and swq(maxima=A + 1) == _lib.EALIGN
+    assert swq(act=A + 2) == _lib.EALIGN
+    assert swq(m=0) == _lib.OK
     # linear_quantize_with_max(x, maxima, m, k, q, scales, w, ws, n, residual, out, combined, dtype)
     qm = lambda **kw: L.w8a8_linear_quantize_with_max(  # noqa: E731
         None, kw.get("x", A), kw.get("maxima", A), kw.get("m", 1), 12288, A, A, A, A, 4096,
@@ -298,6 +310,12 @@ def test_module_grouped_and_swiglu_check_operand_lengths():
         mod.linear_swiglu(None, None, q, asc, k, short, ws, out, good, ws, out, out, None)
     with pytest.raises(ValueError, match="q"):
         mod.linear_swiglu(None, None, _fake(k, np.int8), asc, k, good, ws, out, good, ws, out, out, None)
+    mx, qo, so = _fake(m, np.uint32), _fake(m * n, np.int8), _fake(m, np.float32)
+    with pytest.raises(ValueError, match="w_up"):
+        mod.linear_swiglu_quantize(None, None, q, asc, k, good, ws, out, short, ws, out, out, mx, qo, so)
+    with pytest.raises(ValueError, match="q_out"):
+        mod.linear_swiglu_quantize(None, None, q, asc, k, good, ws, out, good, ws, out, out, mx,
+                                   _fake(m * n - 1, np.int8), so)
 
 
 @pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
