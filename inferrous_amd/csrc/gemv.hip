@@ -169,47 +169,48 @@ __global__ __launch_bounds__(kFinalizeThreads) void select_finalize(const uint64
   }
 }
 
-// M = 1, k = KC * 1024 known at compile time: activations held in registers.
-// WV waves per workgroup.  SINGLE (one matrix): the matrix index is the
-// constant 0 and the grid's tail waves clamp their rows rather than branch, so
-// every kernel-argument load has a fixed offset and no branch in front of it
-// and they issue as one batch -- measured on MI355X, the dependent chain of
-// the sibling lookup costs 0.3-0.7 us per launch on the decode shapes.
-template <int R, int KC, int EPI, int WV = kGemvWaves, bool SINGLE = false>
-__global__ __launch_bounds__(64 * WV) void gemv_m1(GemvArgs a) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t g = blockIdx.x * WV + wave_id();
-  const bool live = SINGLE || g < total_groups(a);
-  const int mi = SINGLE ? 0 : live ? owner(a, g) : 0;
-  const uint32_t n = pick(a.n, mi);
-  const uint32_t row0 = SINGLE ? g * R : live ? (g - pick(a.gbegin, mi)) * R : 0;
-  void* const out = pick(a.out, mi);
-  constexpr uint32_t K = KC * 1024;
-  __shared__ SelectLds<WV> sel;
-  if (EPI == EPI_ARGMAX) select_lds_init(sel);
+// Operands of one M = 1 row-group wave, resolved by the kernel entry.
+struct M1Operands {
+  const int8_t* q;
+  const float* asc;
+  const int8_t* w;
+  const float* ws;
+  uint32_t n;     // rows of the owning matrix (>= 1 when live)
+  uint32_t row0;  // first row of this wave's group
+  bool live;
+  void* out;
+  int dtype;
+  const float* residual;  // EPI_RESIDUAL
+  void* combined;
+};
 
+// M = 1, k = KC * 1024 known at compile time: activations held in registers.
+// R consecutive rows per wave; `sel` and `slots` serve the fused selection.
+template <int R, int KC, int EPI, int WV>
+__device__ __forceinline__ void gemv_m1_body(const M1Operands& o, SelectLds<WV>* sel, uint64_t* slots) {
+  const int lane = threadIdx.x & 63;
+  constexpr uint32_t K = KC * 1024;
   int acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0;
   float wsc = 0.f;  // ws of this lane's output row (writer lanes)
   float asc = 0.f;
   float resid = 0.f;
-  if (live) {
-    const int8_t* __restrict__ W = pick(a.w, mi);
+  if (o.live) {
     v4i x[KC];
 #pragma unroll
-    for (int c = 0; c < KC; ++c) x[c] = load16(a.q + c * 1024 + lane * 16);
+    for (int c = 0; c < KC; ++c) x[c] = load16(o.q + c * 1024 + lane * 16);
     // The epilogue's operands are loaded ahead of the weight stream, so that
     // their latency hides under it instead of extending the wave's life.
-    const uint32_t erow = min(row0 + (uint32_t)min(lane, R - 1), n - 1);
-    wsc = pick(a.ws, mi)[erow];
-    asc = a.asc[0];
-    if (EPI == EPI_RESIDUAL) resid = a.residual[erow];
+    const uint32_t erow = min(o.row0 + (uint32_t)min(lane, R - 1), o.n - 1);
+    wsc = o.ws[erow];
+    asc = o.asc[0];
+    if (EPI == EPI_RESIDUAL) resid = o.residual[erow];
     v4i wv[R][KC];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint32_t row = min(row0 + r, n - 1);  // tail rows recompute the last row
-      const int8_t* p = W + (size_t)row * K + lane * 16;
+      const uint32_t row = min(o.row0 + r, o.n - 1);  // tail rows recompute the last row
+      const int8_t* p = o.w + (size_t)row * K + lane * 16;
 #pragma unroll
       for (int c = 0; c < KC; ++c) wv[r][c] = load_nt16(p + c * 1024);
     }
@@ -219,19 +220,75 @@ __global__ __launch_bounds__(64 * WV) void gemv_m1(GemvArgs a) {
       for (int c = 0; c < KC; ++c) acc[r] = dot16(x[c], wv[r][c], acc[r]);
   }
   const int total = reduce_to_lanes<R>(acc, lane);
-  const uint32_t row = row0 + lane;
-  const bool writer = live && lane < R && row < n;
+  const uint32_t row = o.row0 + lane;
+  const bool writer = o.live && lane < R && row < o.n;
   // Computed on every lane and pinned here, so the compiler cannot sink the
   // operand loads above into the writer branch, behind the weight stream.
-  float value = dequant(total, asc, wsc);
-  float comb = EPI == EPI_RESIDUAL ? bf16_rne(resid + value) : 0.f;
-  const int dtype = a.out_dtype;
+  const float value = dequant(total, asc, wsc);
+  const float comb = EPI == EPI_RESIDUAL ? bf16_rne(resid + value) : 0.f;
+  const int dtype = o.dtype;
   asm volatile("" ::"v"(value), "v"(comb), "s"(dtype));
   if (writer) {
-    if (out) store_out(out, row, dtype, total, value);
-    if (EPI == EPI_RESIDUAL) store_out(a.combined, row, dtype, total, comb);
+    if (o.out) store_out(o.out, row, dtype, total, value);
+    if (EPI == EPI_RESIDUAL) store_out(o.combined, row, dtype, total, comb);
   }
-  if (EPI == EPI_ARGMAX) select_publish_wave(writer ? select_key(value, row) : 0ull, sel, a.slots);
+  if (EPI == EPI_ARGMAX) select_publish_wave(writer ? select_key(value, row) : 0ull, *sel, slots);
+}
+
+// Generic entry: up to kMaxGroup sibling matrices, and the fused selection.
+template <int R, int KC, int EPI, int WV = kGemvWaves>
+__global__ __launch_bounds__(64 * WV) void gemv_m1(GemvArgs a) {
+  const uint32_t g = blockIdx.x * WV + wave_id();
+  __shared__ SelectLds<WV> sel;
+  M1Operands o;
+  o.live = g < total_groups(a);
+  const int mi = o.live ? owner(a, g) : 0;
+  o.q = a.q;
+  o.asc = a.asc;
+  o.w = pick(a.w, mi);
+  o.ws = pick(a.ws, mi);
+  o.n = pick(a.n, mi);
+  o.row0 = o.live ? (g - pick(a.gbegin, mi)) * R : 0;
+  o.out = pick(a.out, mi);
+  o.dtype = a.out_dtype;
+  o.residual = a.residual;
+  o.combined = a.combined;
+  if (EPI == EPI_ARGMAX) {
+    // The selection's LDS counter is zeroed behind a barrier.  The barrier
+    // follows the argument loads (pinned here), so that the waves leave it
+    // together and go straight to the weight stream: measured on MI355X for
+    // the 151,936 x 4096 head, 88.9-89.1 us per launch this way against
+    // 92.4-96.0 with the barrier first.
+    asm volatile("" ::"s"(o.n), "s"(o.w), "s"(o.row0));
+    select_lds_init(sel);
+  }
+  gemv_m1_body<R, KC, EPI, WV>(o, &sel, a.slots);
+}
+
+// One matrix (plain or residual epilogue), with scalar kernel arguments:
+// the build preloads the first 16 argument dwords -- all of these -- into
+// SGPRs, so the waves issue their loads without a kernel-argument load.
+// The grid's tail waves clamp their rows rather than branch.  Measured on
+// MI355X against the generic entry, the sibling lookup's chain of dependent
+// argument loads cost 0.3-0.7 us per decode launch.
+template <int R, int KC, int EPI, int WV = kGemvWaves>
+__global__ __launch_bounds__(64 * WV) void gemv_m1_one(const int8_t* w, const int8_t* q, const float* ws,
+                                                       const float* asc, void* out, uint32_t n, int dtype,
+                                                       const float* residual, void* combined) {
+  static_assert(EPI != EPI_ARGMAX, "the fused selection takes the generic entry");
+  M1Operands o;
+  o.q = q;
+  o.asc = asc;
+  o.w = w;
+  o.ws = ws;
+  o.n = n;
+  o.row0 = (blockIdx.x * WV + wave_id()) * R;
+  o.live = true;
+  o.out = out;
+  o.dtype = dtype;
+  o.residual = residual;
+  o.combined = combined;
+  gemv_m1_body<R, KC, EPI, WV>(o, nullptr, nullptr);
 }
 
 // Any m (blockIdx.y selects MT activation rows), any k % 16 == 0.
@@ -515,13 +572,16 @@ static hipError_t launch_m1(hipStream_t st, GemvArgs& a, const uint32_t* nn, uin
   const uint32_t groups = count_groups<R>(a, nn, a.count);
   *blocks = (groups + W - 1) / W;
   if (groups == 0) return hipSuccess;
-  // The fused selection keeps the generic prologue: measured on MI355X for
-  // the 151,936 x 4096 head, its 16-wave workgroups take 89.2-89.3 us per
-  // launch with it and 90.4-96.8 us with the single-matrix one.
-  if (a.count == 1 && EPI != EPI_ARGMAX)
-    hipLaunchKernelGGL((gemv_m1<R, KC, EPI, W, true>), dim3(*blocks), dim3(64 * W), 0, st, a);
-  else
-    hipLaunchKernelGGL((gemv_m1<R, KC, EPI, W, false>), dim3(*blocks), dim3(64 * W), 0, st, a);
+  // The fused selection keeps the generic entry, which orders its barrier
+  // after the argument loads.
+  if constexpr (EPI != EPI_ARGMAX) {
+    if (a.count == 1) {
+      hipLaunchKernelGGL((gemv_m1_one<R, KC, EPI, W>), dim3(*blocks), dim3(64 * W), 0, st, a.w[0], a.q,
+                         a.ws[0], a.asc, a.out[0], a.n[0], a.out_dtype, a.residual, a.combined);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((gemv_m1<R, KC, EPI, W>), dim3(*blocks), dim3(64 * W), 0, st, a);
   return hipGetLastError();
 }
 
