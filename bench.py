@@ -417,7 +417,7 @@ def main() -> int:
     log(f"dispatch gap {gap_us:.2f} us/launch; in-kernel rate {in_kernel_gbs:.0f} GB/s")
 
     # ------------------------------------------------------------ roofline
-    # Dominant kernel: gemv_m1<1,4,0,4>, the gate_up GEMV (24576 x 4096, one row
+    # Dominant kernel: gemv_m1_one<1,4,0,4>, the gate_up GEMV (24576 x 4096, one row
     # per wave) -- the largest share of the step.  Timed as a graph of the 36
     # distinct-weight launches of one token, HIP events on the launch stream.
     gu = [mats[2] for mats in layers]
@@ -430,7 +430,7 @@ def main() -> int:
     dom_ms = time_graph(capture(gate_up_chain), max(10, args.steps // 2))
     dom_avg_us = dom_ms * 1e3 / len(gu)
     dom_gbs = gu_bytes / (dom_avg_us * 1e-6) / 1e9
-    roofline = {"kernel": "gemv_m1<1,4,0,4> (gate_up 24576x4096, M=1)", "bound": "hbm",
+    roofline = {"kernel": "gemv_m1_one<1,4,0,4> (gate_up 24576x4096, M=1)", "bound": "hbm",
                 "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                 "avg_launch_us": round(dom_avg_us, 3), "bytes_per_launch": gu_bytes}
