@@ -197,6 +197,61 @@ def test_linear_residual(env, fixtures):
                 assert np.array_equal(cb, (bits(comb_want) >> 16).astype(np.uint16))
 
 
+@pytest.mark.parametrize("k,n", [(4096, 8191), (4096, 8192), (4096, 8193), (4096, 12289), (12288, 4097),
+                                 (12288, 3)])
+def test_decode_gemv_one_matrix_routes(env, k, n):
+    """M = 1 on one matrix runs the scalar-argument GEMV entry: two rows per
+    wave up to N = 8192 at K = 4096, one row per wave above that and at
+    K = 12288.  These N leave the last workgroup partly empty, so its tail
+    waves clamp their rows to the last one and must not write.  Every output
+    dtype, the residual epilogue (src/kernels.rs:577-618) in f32 and BF16,
+    and a one-member grouped call (the same entry) against the oracle; each
+    output sits in a larger buffer whose guard elements past N must come
+    back untouched."""
+    ctx, mod, s = env
+    rng = np.random.default_rng(9100 + n + k)
+    q = rng.integers(-127, 128, size=(1, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    w[-1, :] = -127                          # the row the tail waves clamp to
+    asc = np.array([rng.random() / 64 + 1e-4], F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    acc, out, outb = oracle.linear(q, asc, w, ws, k)
+    res = rng.standard_normal(n).astype(F32)
+    comb = oracle.residual(res, out.reshape(-1))
+    dq, da, dw, dws, dres = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws), dev(s, res)
+    guard = 64
+
+    def guarded(dtype):
+        fill = np.full(n + guard, 0x5A5A, dtype)
+        base = DeviceBuffer.from_host(s, fill)
+        return base, DeviceBuffer.view_of(base, 0, n)
+
+    def check(base, exp, what):
+        got = base.to_host_vec(s)
+        if got.dtype == np.float32:
+            assert np.array_equal(bits(got[:n]), bits(exp.reshape(-1))), what
+        else:
+            assert np.array_equal(got[:n], exp.reshape(-1)), what
+        assert np.all(got[n:] == got.dtype.type(0x5A5A)), f"{what}: write past N"
+
+    for dtype, exp in ((np.int32, acc), (np.uint16, outb), (np.float32, out)):
+        base, o = guarded(dtype)
+        mod.linear(s, None, dq, da, dw, dws, k, o)
+        check(base, exp, f"linear {np.dtype(dtype)}")
+        base, o = guarded(dtype)
+        mod.linear_grouped(s, dq, da, k, [(dw, dws, o)])
+        check(base, exp, f"grouped(1) {np.dtype(dtype)}")
+    for dtype in (np.float32, np.uint16):
+        (bo, o), (bc, c) = guarded(dtype), guarded(dtype)
+        mod.linear_residual(s, None, dq, da, dw, dws, k, dres, o, c, k)
+        if dtype is np.float32:
+            check(bo, out, "residual out f32")
+            check(bc, comb, "residual combined f32")
+        else:
+            check(bo, (bits(out) >> 16).astype(np.uint16), "residual out bf16")
+            check(bc, (bits(comb) >> 16).astype(np.uint16), "residual combined bf16")
+
+
 def test_pair_triple_share_activations(env, fixtures):
     """src/conformance.rs:263-300: the same matrix in every sibling slot
     reproduces the single projection bit for bit."""
