@@ -345,7 +345,7 @@ __device__ __forceinline__ void store_blocks(const GemmArgs& a, const v16i (&acc
 // hit sixteen different 16-byte bank groups.  Sub-step i of a stage covers
 // k bytes [32i, 32i + 32): lane l (row / column l % 32, half h = l / 32)
 // reads chunk 2i + h -- the same lane -> k map for A and B.
-template <int BM, int BN, int WM, int WN, int SA, int SB, int EP>
+template <int BM, int BN, int WM, int WN, int SA, int SB, int EP, bool ROT = false>
 __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, uint32_t tiles_n,
                                                 uint32_t splits) {
   constexpr int WAVES_N = BN / WN;
@@ -395,13 +395,19 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
     const uint32_t g = n0 + row;
     srcB[j] = a.w + (size_t)(g < a.n ? g : 0) * K + kbase + ((lane & 7) ^ ((row >> 1) & 7)) * 16;
   }
+  // ROT: stage kt reads global K chunk (kt + rot) mod KT, rot = tile mod KT.
+  const uint32_t rot = ROT ? Lt % KT : 0;
+  auto kc = [&](uint32_t kt) -> size_t {
+    const uint32_t c = kt + rot;
+    return (size_t)(c >= KT ? c - KT : c) * 128;
+  };
   auto loadA = [&](uint32_t kt, int j) {
-    __builtin_amdgcn_global_load_lds((const void*)(srcA[j] + (size_t)kt * 128),
+    __builtin_amdgcn_global_load_lds((const void*)(srcA[j] + kc(kt)),
                                      W8A8_LDS_PTR(ldsA + (kt % SA) * ASL + (wave * LA + j) * 1024 + lane * 16),
                                      16, 0, 0);
   };
   auto loadB = [&](uint32_t kt, int j) {
-    __builtin_amdgcn_global_load_lds((const void*)(srcB[j] + (size_t)kt * 128),
+    __builtin_amdgcn_global_load_lds((const void*)(srcB[j] + kc(kt)),
                                      W8A8_LDS_PTR(ldsB + (kt % SB) * BSL + (wave * LB + j) * 1024 + lane * 16),
                                      16, 0, 0);
   };
@@ -487,6 +493,19 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   store_blocks<EP, FM, FN>(a, acc, m0 + wm0, n0 + wn0, lane);
 }
 
+// Unsplit launches rotate each workgroup's K order (stage kt reads K chunk
+// (kt + tile) mod KT; the i32 sums are exact in any order, so outputs are
+// bit-identical).  Otherwise every workgroup reads the same 128-byte column
+// of its 4 KiB weight rows at the same time.  Measured on MI355X (graphs of 16
+// distinct-weight launches): gate_up 24576 x 4096 at M = 64 22.2 against
+// 25.1 us, M = 100 33.8 against 35.2, M = 129 29.4-29.7 against 30.3-31.4,
+// M = 193 32.8 against 34.5-35.0, M = 300 51.7-53.3 against 54.2-54.8,
+// M = 512 54.6-56.1 against 56.0-58.8; qkv at M = 512 21.9-22.5 against
+// 22.3-22.7; o level.  Split-K launches, whose slabs already start at
+// different K offsets, measured level or up to 1.3% slower rotated, and keep
+// the order.
+constexpr bool kRotateK = true;
+
 // The residual epilogue holds a residual per accumulator; with a 64 x 96
 // wave tile that is 96 more registers than the kernel has, and it spills.
 // Such tiles take no residual (launch_gemm routes residual outputs to
@@ -499,20 +518,20 @@ static hipError_t launch_dma(hipStream_t st, const GemmArgs& a) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
   const dim3 grid(tm * tn), block(512);
   if (a.out_dtype == W8A8_OUT_I32) {
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32, kRotateK>), grid, block, 0, st, a, tm, tn, 1u);
   } else if (a.residual) {
     if constexpr (kResidualTile<WM, WN>) {
       if (a.out_dtype == W8A8_OUT_F32)
-        hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32_RES>), grid, block, 0, st, a, tm, tn, 1u);
+        hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32_RES, kRotateK>), grid, block, 0, st, a, tm, tn, 1u);
       else
-        hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16_RES>), grid, block, 0, st, a, tm, tn, 1u);
+        hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16_RES, kRotateK>), grid, block, 0, st, a, tm, tn, 1u);
     } else {
       return hipErrorInvalidValue;
     }
   } else if (a.out_dtype == W8A8_OUT_F32) {
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_F32, kRotateK>), grid, block, 0, st, a, tm, tn, 1u);
   } else {
-    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16>), grid, block, 0, st, a, tm, tn, 1u);
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_BF16, kRotateK>), grid, block, 0, st, a, tm, tn, 1u);
   }
   return hipGetLastError();
 }
@@ -571,7 +590,7 @@ __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
 // and counts its waits with its own na, nb.  During stage kt it issues
 // A(kt + SA - 1), then B(kt + SB - 1).
 // Split-K as in gemm_dma: workgroup (tile, split) writes i32 slab `split`.
-template <int BN, int SA, int SB, int MA, int EP>
+template <int BN, int SA, int SB, int MA, int EP, bool ROT = false>
 __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, uint32_t splits) {
   constexpr int FN = BN / 32;
   constexpr int ASL = MA * 128, BSL = BN * 128;
@@ -615,11 +634,19 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
     const uint32_t br = 8 * (wave + 8 * j) + (lane >> 3);  // row within the weight tile
     srcB[j] = a.w + (size_t)min(n0 + br, a.n - 1) * K + kbase + ((lane & 7) ^ ((br >> 1) & 7)) * 16;
   }
+  // ROT: stage kt reads global K chunk (kt + rot) mod KT, rot = Lt mod KT, so
+  // the workgroups do not all read the same 128-byte column of their weight
+  // rows at once.
+  const uint32_t rot = ROT ? Lt % KT : 0;
+  auto kc = [&](uint32_t kt) -> size_t {
+    const uint32_t c = kt + rot;
+    return (size_t)(c >= KT ? c - KT : c) * 128;
+  };
   auto issueA = [&](uint32_t kt) {
 #pragma unroll
     for (int j = 0; j < kMaxA; ++j)
       if (j < na)
-        __builtin_amdgcn_global_load_lds((const void*)(srcA[j] + (size_t)kt * 128),
+        __builtin_amdgcn_global_load_lds((const void*)(srcA[j] + kc(kt)),
                                          W8A8_LDS_PTR(ldsA + (kt % SA) * ASL + 1024 * (wave + 8 * j) + lane * 16),
                                          16, 0, 0);
   };
@@ -627,7 +654,7 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
 #pragma unroll
     for (int j = 0; j < kMaxB; ++j)
       if (j < nb)
-        __builtin_amdgcn_global_load_lds((const void*)(srcB[j] + (size_t)kt * 128),
+        __builtin_amdgcn_global_load_lds((const void*)(srcB[j] + kc(kt)),
                                          W8A8_LDS_PTR(ldsB + (kt % SB) * BSL + 1024 * (wave + 8 * j) + lane * 16),
                                          16, 0, kCpolNT);
   };
@@ -938,7 +965,7 @@ static hipError_t launch_split(hipStream_t st, const GemmArgs& a, uint32_t split
   GemmArgs p = a;
   p.out = a.partials;
   p.out_dtype = W8A8_OUT_I32;
-  hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32>), dim3(tm * tn * splits), dim3(512), 0, st, p,
+  hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32, false>), dim3(tm * tn * splits), dim3(512), 0, st, p,
                      tm, tn, splits);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -953,21 +980,21 @@ static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits
     GemmArgs p = a;
     p.out = a.partials;
     p.out_dtype = W8A8_OUT_I32;
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32>), grid, block, 0, st, p, tn, splits);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32, false>), grid, block, 0, st, p, tn, splits);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_splitk_epilogue(st, a, splits);
   }
   if (a.out_dtype == W8A8_OUT_I32)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32, kRotateK>), grid, block, 0, st, a, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32_RES>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32_RES, kRotateK>), grid, block, 0, st, a, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32, kRotateK>), grid, block, 0, st, a, tn, 1u);
   else if (a.residual)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16_RES>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16_RES, kRotateK>), grid, block, 0, st, a, tn, 1u);
   else
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16, kRotateK>), grid, block, 0, st, a, tn, 1u);
   return hipGetLastError();
 }
 
