@@ -140,8 +140,11 @@ def head_profile_run() -> int:
 def prefill_profile_run() -> int:
     """Workload for a kernel-trace profile of the prefill GEMMs: 8 layers of
     distinct weights (1.5 GB, above the MALL), the four projections at
-    M = 512 and M = 129, three eager passes each (no graphs)."""
+    M = 512 and M = 129, three eager passes each (no graphs); then a 256 MiB
+    device copy three times, the calibration kernel of known traffic for
+    counter passes (reads and writes 256 MiB)."""
     from inferrous_amd import CudaContext, DeviceBuffer, load, synth
+    from inferrous_amd import _lib
     ctx = CudaContext(0)
     mod = load(ctx)
     s = ctx.new_stream()
@@ -168,6 +171,12 @@ def prefill_profile_run() -> int:
                 mod.linear(s, None, pq[k][0], pq[k][1], w, ws, k, outs[name])
         s.synchronize()
         print(f"prefill M={m} done", flush=True)
+    src = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
+    dst = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
+    for _ in range(3):
+        _lib.check(_lib.lib().w8a8_memcpy_dtod(dst.ptr, src.ptr, 256 << 20, s.handle))
+    s.synchronize()
+    print("calibration copies done", flush=True)
     return 0
 
 
