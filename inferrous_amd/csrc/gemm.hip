@@ -501,9 +501,11 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
 // 25.1 us, M = 100 33.8 against 35.2, M = 129 29.4-29.7 against 30.3-31.4,
 // M = 193 32.8 against 34.5-35.0, M = 300 51.7-53.3 against 54.2-54.8,
 // M = 512 54.6-56.1 against 56.0-58.8; qkv at M = 512 21.9-22.5 against
-// 22.3-22.7; o level.  Split-K launches, whose slabs already start at
-// different K offsets, measured level or up to 1.3% slower rotated, and keep
-// the order.
+// 22.3-22.7; o level.  In the 36-layer prefill graphs, where each gate_up
+// follows qkv and o, the M = 512 and M = 129 totals came out level (A/B on
+// one box) while the ragged gate_up at M = 16 went from 4.20 to 4.85 TB/s.
+// Split-K launches, whose slabs already start at different K offsets,
+// measured level or up to 1.3% slower rotated, and keep the order.
 constexpr bool kRotateK = true;
 
 // The residual epilogue holds a residual per accumulator; with a 64 x 96
