@@ -324,11 +324,20 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
       xrow[t] = a.q + (size_t)(xok[t] ? m0 + t : 0) * K;
     }
     const uint32_t nch = (K + 1023) / 1024;
+    // Up to 4 activation rows per pass, the row group's chunk order starts at
+    // chunk g mod nch (exact sums in any order), so the waves of a launch do
+    // not all read the same 1 KiB column of their rows at once.  Measured on
+    // MI355X: gate_up 24576 x 4096 at M = 2 5.13 -> 5.65-5.76 TB/s, at M = 4
+    // 4.58 -> 4.81-4.85; down 4096 x 12288 at M = 4 3.34 -> 3.48-3.51.  The
+    // 8-row form (M >= 8, where the MFMA family is routed) lost 5-9% rotated.
+    const uint32_t rot = MT <= 4 ? g % nch : 0;
     for (uint32_t c = 0; c < nch; c += U) {
       v4i wv[U][R], xv[U][MT];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const uint32_t kk = (c + u) * 1024 + lane * 16;
+        uint32_t ci = c + u + rot;
+        ci = ci >= nch ? ci - nch : ci;
+        const uint32_t kk = ci * 1024 + lane * 16;
         const bool ok = (c + u < nch) && kk < K;
 #pragma unroll
         for (int r = 0; r < R; ++r) wv[u][r] = ok ? load_nt16(wrow[r] + kk) : v4i{0, 0, 0, 0};
