@@ -55,7 +55,8 @@ extern "C" {
  * w8a8_linear uses */
 #define W8A8_PATH_AUTO 0
 #define W8A8_PATH_DOT4 1 /* v_dot4 GEMV, wave per row group           */
-#define W8A8_PATH_MFMA 2 /* LDS-staged v_mfma_i32_16x16x64_i8 GEMM    */
+#define W8A8_PATH_MFMA 2 /* LDS-staged MFMA GEMM (v_mfma_i32_32x32x32_i8,
+                            16x16x64_i8 for 3 <= M < 8)               */
 
 /* ------------------------------------------------------------------ runtime
  * Replaces cuda_core's CudaContext::new / new_stream / DeviceBuffer /

@@ -63,10 +63,12 @@ int check_linear(const int8_t* q, const float* asc, size_t m, const int8_t* w, c
   return W8A8_OK;
 }
 
-// dot4 GEMV for m <= 2, MFMA beyond: the measured crossover on MI355X
-// (gate_up / down at m = 1..64) lies between m = 4 and m = 8; at m = 3..4
-// the two families are within 1%.
-constexpr size_t kDot4MaxM = 2;
+// dot4 GEMV for m <= 4, MFMA beyond: the measured crossover on MI355X
+// (gate_up / down at m = 1..64) lies between m = 4 and m = 8.  At m = 4 the
+// dot4 GEMV (chunk order rotated per row group) streams gate_up at 4.8 TB/s
+// and down at 3.5 against the MFMA family's 4.4 and 3.0; at m = 8 the MFMA
+// family leads, 4.86 / 3.37 against 3.62 / 2.79.
+constexpr size_t kDot4MaxM = 4;
 
 int run_linear(hipStream_t st, const int8_t* q, const float* asc, size_t m, const int8_t* w,
                const float* ws, size_t n, uint32_t k, void* out, int out_dtype, int path,
