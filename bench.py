@@ -281,6 +281,70 @@ def chain_profile_run() -> int:
     return 0
 
 
+def timeline_run() -> int:
+    """Where a decode GEMV launch spends its time, without a profiler.  For
+    each decode shape, 36 distinct-weight launches of the timed one-matrix
+    M = 1 GEMV (w8a8_diag_linear_timeline: the kernel body and launch shape
+    of w8a8_linear, plus per-wave stamps of the 100 MHz device clock) are
+    captured as one graph and replayed 20 times.  From the last replay, per
+    launch: `gap`, the previous launch's last wave end to this launch's first
+    wave start; `first` and `last`, the first wave start to the first and to
+    the last wave whose loads have all landed; `tail`, the last landing to
+    the last acknowledged store; `launch`, end to end; `TB/s`, the launch's
+    bytes over `last`.  Medians over launches 2..35; one line per shape."""
+    from inferrous_amd import CudaContext, DeviceBuffer, Graph, load, synth
+    from inferrous_amd import _lib
+    ctx = CudaContext(0)
+    mod = load(ctx)
+    s = ctx.new_stream()
+    L = _lib.lib()
+    nl, tick_us = 36, 0.01   # s_memrealtime: 100 MHz
+    print(f"{'shape':8s} {'N x K':>12s} {'waves':>6s} {'gap':>6s} {'first':>6s} {'last':>6s} {'tail':>6s} "
+          f"{'launch':>7s} {'TB/s':>6s}   (us, medians of launches 2..35)", flush=True)
+    for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
+        mats = []
+        for layer in range(nl):
+            w = DeviceBuffer.zeroed(s, n * k, np.int8)
+            ws = DeviceBuffer.zeroed(s, n, np.float32)
+            mod.synth_i8(s, w, SEED_W, synth.weight_stream(layer, si))
+            mod.synth_f32(s, ws, SEED_S, synth.scale_stream(layer, si), 1e-3, 1e-2)
+            mats.append((w, ws))
+        x = DeviceBuffer.from_host(s, synth.normal_rows(40, 1, k).reshape(-1))
+        q, sc = DeviceBuffer.zeroed(s, k, np.int8), DeviceBuffer.zeroed(s, 1, np.float32)
+        mod.quantize(s, None, x, k, q, sc)
+        out = DeviceBuffer.zeroed(s, n, np.uint16)
+        need = L.w8a8_diag_linear_timeline_stamps(n, k)
+        stamps = DeviceBuffer.zeroed(s, nl * need, np.uint64)
+
+        def launches():
+            for i, (w, ws) in enumerate(mats):
+                _lib.check(L.w8a8_diag_linear_timeline(s.handle, q.ptr, sc.ptr, w.ptr, ws.ptr, n, k, out.ptr,
+                                                       _lib.OUT_BF16, stamps.ptr + i * need * 8, need),
+                           "diag_linear_timeline")
+        launches()
+        s.synchronize()
+        g = Graph(s)
+        with g:
+            launches()
+        for _ in range(20):
+            g.launch()
+        s.synchronize()
+        t = stamps.to_host_vec(s).astype(np.int64).reshape(nl, need // 3, 3)
+        start, landed, end = t[:, :, 0].min(1), t[:, :, 1], t[:, :, 2].max(1)
+        first, last = landed.min(1), landed.max(1)
+        gap = (start[1:] - end[:-1])[1:] * tick_us
+        to_first = (first - start)[2:] * tick_us
+        to_last = (last - start)[2:] * tick_us
+        tail = (end - last)[2:] * tick_us
+        launch = (end[1:] - end[:-1])[1:] * tick_us
+        med = lambda a: float(np.median(a))
+        rate = gemv_bytes(n, k) / (med(to_last) * 1e-6) / 1e12
+        print(f"{name:8s} {n:>5d} x {k:<5d} {need // 3:6d} {med(gap):6.2f} {med(to_first):6.2f} {med(to_last):6.2f} "
+              f"{med(tail):6.2f} {med(launch):7.2f} {rate:6.2f}", flush=True)
+        del mats, stamps, g
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,6 +362,8 @@ def main() -> int:
                     help="run only the decode layer chain workload for a kernel-trace profile")
     ap.add_argument("--ragged-profile", action="store_true",
                     help="run only the ragged small-batch workload for a kernel-trace profile")
+    ap.add_argument("--timeline", action="store_true",
+                    help="run only the per-wave clock timeline of the decode GEMV launches")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode "
@@ -313,6 +379,8 @@ def main() -> int:
         return head_profile_run()
     if args.ragged_profile:
         return ragged_profile_run()
+    if args.timeline:
+        return timeline_run()
     if args.chain_profile:
         return chain_profile_run()
 

@@ -88,6 +88,14 @@ class W8A8Error(RuntimeError):
         super().__init__(f"{what}: status {status} ({msg})" if what else f"status {status} ({msg})")
 
 
+# Diagnostics declared in include/inferrous_w8a8_diag.h (no reference
+# counterpart; used by bench.py --timeline).
+DIAG_SIGNATURES: dict[str, tuple] = {
+    "w8a8_diag_linear_timeline_stamps": (S, [S, U32]),
+    "w8a8_diag_linear_timeline": (I, [P, P, P, P, P, S, U32, P, I, P, S]),
+}
+
+
 def lib() -> ctypes.CDLL:
     """Load the HIP library (once).  Raises if it has not been built."""
     global _lib
@@ -96,7 +104,7 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(
                 f"HIP library not found at {LIB_PATH}; build it with `python -m inferrous_amd.build`")
         L = ctypes.CDLL(str(LIB_PATH))
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in {**SIGNATURES, **DIAG_SIGNATURES}.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args

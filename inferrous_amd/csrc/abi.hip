@@ -14,6 +14,7 @@
 #include <mutex>
 
 #include "../../include/inferrous_w8a8.h"
+#include "../../include/inferrous_w8a8_diag.h"
 #include "internal.hpp"
 
 using namespace w8a8;
@@ -703,6 +704,27 @@ int w8a8_linear_argmax_noalloc(void* stream, const int8_t* q, const float* asc, 
                     static_cast<uint64_t*>(keys));
 }
 
+
+size_t w8a8_diag_linear_timeline_stamps(size_t n, uint32_t k) {
+  if (n > kU32Max) return 0;
+  return 3 * gemv_timeline_waves(n, k);
+}
+
+int w8a8_diag_linear_timeline(void* stream, const int8_t* q, const float* asc, const int8_t* w,
+                              const float* ws, size_t n, uint32_t k, void* out, int out_dtype,
+                              uint64_t* stamps, size_t stamps_len) {
+  const int c = check_linear(q, asc, 1, w, ws, n, k, out, out_dtype);
+  if (c != W8A8_OK) return c;
+  if (n == 0) return W8A8_OK;
+  const size_t need = w8a8_diag_linear_timeline_stamps(n, k);
+  if (need == 0) return W8A8_ESHAPE;  // k other than 4096 / 12288
+  if (!stamps) return W8A8_ENULL;
+  if (!al(stamps, 8)) return W8A8_EALIGN;
+  if (stamps_len < need) return W8A8_EWORKSPACE;
+  if (!ready()) return W8A8_EINIT;
+  return hip_status(launch_gemv_timeline((hipStream_t)stream, q, asc, w, ws, (uint32_t)n, k, out, out_dtype,
+                                         stamps));
+}
 
 int w8a8_synth_i8(void* stream, int8_t* out, size_t n, uint64_t seed, uint64_t stream_id) {
   if (n == 0) return W8A8_OK;

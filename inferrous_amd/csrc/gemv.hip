@@ -186,8 +186,14 @@ struct M1Operands {
 
 // M = 1, k = KC * 1024 known at compile time: activations held in registers.
 // R consecutive rows per wave; `sel` and `slots` serve the fused selection.
-template <int R, int KC, int EPI, int WV>
-__device__ __forceinline__ void gemv_m1_body(const M1Operands& o, SelectLds<WV>* sel, uint64_t* slots) {
+// TIMED (diagnostics only): the wave also records the 100 MHz device clock
+// at its start, once all its loads have landed, and once its store is
+// acknowledged, into stamps[3 g .. 3 g + 2] (g: the wave's index in the grid).
+template <int R, int KC, int EPI, int WV, bool TIMED = false>
+__device__ __forceinline__ void gemv_m1_body(const M1Operands& o, SelectLds<WV>* sel, uint64_t* slots,
+                                             uint64_t* stamps = nullptr) {
+  uint64_t t0 = 0, t1 = 0;
+  if constexpr (TIMED) t0 = __builtin_amdgcn_s_memrealtime();
   const int lane = threadIdx.x & 63;
   constexpr uint32_t K = KC * 1024;
   int acc[R];
@@ -214,6 +220,10 @@ __device__ __forceinline__ void gemv_m1_body(const M1Operands& o, SelectLds<WV>*
 #pragma unroll
       for (int c = 0; c < KC; ++c) wv[r][c] = load_nt16(p + c * 1024);
     }
+    if constexpr (TIMED) {
+      __builtin_amdgcn_s_waitcnt(0);
+      t1 = __builtin_amdgcn_s_memrealtime();
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -233,6 +243,16 @@ __device__ __forceinline__ void gemv_m1_body(const M1Operands& o, SelectLds<WV>*
     if (EPI == EPI_RESIDUAL) store_out(o.combined, row, dtype, total, comb);
   }
   if (EPI == EPI_ARGMAX) select_publish_wave(writer ? select_key(value, row) : 0ull, *sel, slots);
+  if constexpr (TIMED) {
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint64_t t2 = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) {
+      const size_t g = (size_t)blockIdx.x * WV + wave_id();
+      stamps[3 * g] = t0;
+      stamps[3 * g + 1] = t1;
+      stamps[3 * g + 2] = t2;
+    }
+  }
 }
 
 // Generic entry: up to kMaxGroup sibling matrices, and the fused selection.
@@ -289,6 +309,26 @@ __global__ __launch_bounds__(64 * WV) void gemv_m1_one(const int8_t* w, const in
   o.residual = residual;
   o.combined = combined;
   gemv_m1_body<R, KC, EPI, WV>(o, nullptr, nullptr);
+}
+
+// Diagnostics: gemv_m1_one (plain epilogue) with the per-wave clock stamps.
+template <int R, int KC>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_m1_timed(const int8_t* w, const int8_t* q, const float* ws,
+                                                                 const float* asc, void* out, uint32_t n, int dtype,
+                                                                 uint64_t* stamps) {
+  M1Operands o;
+  o.q = q;
+  o.asc = asc;
+  o.w = w;
+  o.ws = ws;
+  o.n = n;
+  o.row0 = (blockIdx.x * kGemvWaves + wave_id()) * R;
+  o.live = true;
+  o.out = out;
+  o.dtype = dtype;
+  o.residual = nullptr;
+  o.combined = nullptr;
+  gemv_m1_body<R, KC, EPI_PLAIN, kGemvWaves, true>(o, nullptr, nullptr, stamps);
 }
 
 // Any m (blockIdx.y selects MT activation rows), any k % 16 == 0.
@@ -622,6 +662,32 @@ static hipError_t dispatch(hipStream_t st, GemvArgs& a, uint32_t* blocks) {
   if (a.m <= 2) return launch_mt<2, 4, EPI>(st, a, nn, blocks);
   if (a.m <= 4) return launch_mt<4, 2, EPI>(st, a, nn, blocks);
   return launch_mt<8, 2, EPI>(st, a, nn, blocks);
+}
+
+// The one-matrix M = 1 launch shape of `dispatch` (rows per wave by total N,
+// four waves per workgroup), for the timed diagnostics kernel.
+size_t gemv_timeline_waves(size_t n, uint32_t k) {
+  if (n == 0 || (k != 4096 && k != 12288)) return 0;
+  const size_t r = (k == 4096 && n <= 8192) ? 2 : 1;
+  const size_t groups = (n + r - 1) / r;
+  return (groups + kGemvWaves - 1) / kGemvWaves * kGemvWaves;
+}
+
+hipError_t launch_gemv_timeline(hipStream_t st, const int8_t* q, const float* asc, const int8_t* w,
+                                const float* ws, uint32_t n, uint32_t k, void* out, int dtype,
+                                uint64_t* stamps) {
+  const uint32_t blocks = (uint32_t)(gemv_timeline_waves(n, k) / kGemvWaves);
+  if (blocks == 0) return hipErrorInvalidValue;
+  if (k == 12288)
+    hipLaunchKernelGGL((gemv_m1_timed<1, 12>), dim3(blocks), dim3(kGemvThreads), 0, st, w, q, ws, asc, out, n,
+                       dtype, stamps);
+  else if (n <= 8192)
+    hipLaunchKernelGGL((gemv_m1_timed<2, 4>), dim3(blocks), dim3(kGemvThreads), 0, st, w, q, ws, asc, out, n,
+                       dtype, stamps);
+  else
+    hipLaunchKernelGGL((gemv_m1_timed<1, 4>), dim3(blocks), dim3(kGemvThreads), 0, st, w, q, ws, asc, out, n,
+                       dtype, stamps);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a) {

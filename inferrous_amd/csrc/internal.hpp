@@ -86,6 +86,11 @@ hipError_t launch_norm_quantize(hipStream_t st, const float* x, const float* gai
                                 float* out, int8_t* q, float* scales, uint32_t* maxima);  // width 4096
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a);
+// Diagnostics: the one-matrix M = 1 GEMV with per-wave clock stamps.
+size_t gemv_timeline_waves(size_t n, uint32_t k);
+hipError_t launch_gemv_timeline(hipStream_t st, const int8_t* q, const float* asc, const int8_t* w,
+                                const float* ws, uint32_t n, uint32_t k, void* out, int dtype,
+                                uint64_t* stamps);
 hipError_t launch_gemv_argmax(hipStream_t st, GemvArgs& a);
 hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a);  // m == 1, k in {4096, 12288}
 hipError_t launch_swiglu(hipStream_t st, const void* gate, const void* up, size_t rows,

@@ -16,16 +16,19 @@ from inferrous_amd import _lib
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "inferrous_w8a8.h"
+DIAG_HEADER = ROOT / "include" / "inferrous_w8a8_diag.h"
 
 
-def declared_symbols() -> set[str]:
-    text = HEADER.read_text()
+def declared_symbols(header: Path = HEADER) -> set[str]:
+    text = header.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return set(re.findall(r"\b(w8a8_[a-z0-9_]+)\s*\(", text))
 
 
 def test_header_declarations_match_binding():
     assert declared_symbols() == set(_lib.SIGNATURES)
+    assert declared_symbols(DIAG_HEADER) == set(_lib.DIAG_SIGNATURES)
+    assert not declared_symbols() & declared_symbols(DIAG_HEADER)
 
 
 def declared_arity() -> dict[str, int]:
@@ -52,10 +55,10 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
                          capture_output=True, text=True, check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
-    missing = declared_symbols() - exported
+    missing = (declared_symbols() | declared_symbols(DIAG_HEADER)) - exported
     assert not missing, missing
     L = _lib.lib()
-    for name in declared_symbols():
+    for name in declared_symbols() | declared_symbols(DIAG_HEADER):
         assert getattr(L, name) is not None
 
 
@@ -90,6 +93,41 @@ def no_device_status():
     c = ctypes.c_int()
     _lib.lib().w8a8_device_count(ctypes.byref(c))
     return c.value
+
+
+def test_diag_timeline_stamp_count():
+    """Three stamps per wave of the one-matrix M = 1 launch: two rows per wave
+    up to N = 8192 at K = 4096, one above it and at K = 12288, four waves per
+    workgroup; other widths are not built (0)."""
+    L = _lib.lib()
+    assert L.w8a8_diag_linear_timeline_stamps(6144, 4096) == 3 * 3072
+    assert L.w8a8_diag_linear_timeline_stamps(8193, 4096) == 3 * 8196
+    assert L.w8a8_diag_linear_timeline_stamps(24576, 4096) == 3 * 24576
+    assert L.w8a8_diag_linear_timeline_stamps(4097, 12288) == 3 * 4100
+    assert L.w8a8_diag_linear_timeline_stamps(1, 4096) == 3 * 4
+    assert L.w8a8_diag_linear_timeline_stamps(4096, 1024) == 0
+    assert L.w8a8_diag_linear_timeline_stamps(0, 4096) == 0
+
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_diag_timeline_validation_precedes_device():
+    L = _lib.lib()
+    need = L.w8a8_diag_linear_timeline_stamps(4096, 4096)
+
+    def tl(**kw):
+        a = dict(q=A, asc=A, w=A, ws=A, n=4096, k=4096, out=A, dt=_lib.OUT_BF16, st=A, sl=need)
+        a.update(kw)
+        return L.w8a8_diag_linear_timeline(None, a["q"], a["asc"], a["w"], a["ws"], a["n"], a["k"], a["out"],
+                                           a["dt"], a["st"], a["sl"])
+    assert tl() == _lib.EINIT
+    assert tl(n=0) == _lib.OK
+    assert tl(k=1024) == _lib.ESHAPE
+    assert tl(k=4100) == _lib.ESHAPE
+    assert tl(st=None) == _lib.ENULL
+    assert tl(st=A + 4) == _lib.EALIGN
+    assert tl(sl=need - 1) == _lib.EWORKSPACE
+    assert tl(q=None) == _lib.ENULL
+    assert tl(dt=7) == _lib.EARG
 
 
 @pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")

@@ -252,6 +252,35 @@ def test_decode_gemv_one_matrix_routes(env, k, n):
             check(bc, (bits(comb) >> 16).astype(np.uint16), "residual combined bf16")
 
 
+@pytest.mark.parametrize("k,n", [(4096, 6144), (4096, 8193), (12288, 4097)])
+def test_diag_timeline_matches_linear(env, k, n):
+    """The timed diagnostics GEMV writes the values w8a8_linear writes, and
+    one stamp triple per wave of its launch: start <= loads landed <= store
+    acknowledged, all within the call."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    L = _lib.lib()
+    rng = np.random.default_rng(9300 + n + k)
+    q = rng.integers(-127, 128, size=(1, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    asc = np.array([rng.random() / 64 + 1e-4], F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    dq, da, dw, dws = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws)
+    need = L.w8a8_diag_linear_timeline_stamps(n, k)
+    assert need % 3 == 0 and need // 3 >= (n + 1) // 2
+    want = DeviceBuffer.zeroed(s, n, np.uint16)
+    mod.linear(s, None, dq, da, dw, dws, k, want)
+    got = DeviceBuffer.zeroed(s, n, np.uint16)
+    stamps = DeviceBuffer.zeroed(s, need, np.uint64)
+    _lib.check(L.w8a8_diag_linear_timeline(s.handle, dq.ptr, da.ptr, dw.ptr, dws.ptr, n, k, got.ptr,
+                                           _lib.OUT_BF16, stamps.ptr, need), "diag_linear_timeline")
+    assert np.array_equal(got.to_host_vec(s), want.to_host_vec(s))
+    t = stamps.to_host_vec(s).reshape(-1, 3).astype(np.int64)
+    assert np.all(t[:, 0] > 0)
+    assert np.all(t[:, 0] <= t[:, 1]) and np.all(t[:, 1] <= t[:, 2])
+    assert t[:, 2].max() - t[:, 0].min() < 100_000      # < 1 ms of the 100 MHz clock
+
+
 def test_pair_triple_share_activations(env, fixtures):
     """src/conformance.rs:263-300: the same matrix in every sibling slot
     reproduces the single projection bit for bit."""
