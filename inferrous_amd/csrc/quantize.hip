@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void rounding_probe_kernel(const float* __rest
 // The sum of squares keeps the reference's order exactly: thread t sums
 // RN(x^2) over coordinates t + 256 i (i = 0..15, sequential RN adds), then
 // the halving tree p[t] = RN(p[t] + p[t + d]), d = 128, 64, ..., 1 -- here
-// the first two levels in one wave from LDS, the rest with wave shuffles
+// the first two levels in one wave from LDS, the rest with cross-lane moves
 // (lane 0 only consumes in-range partners).  inv = 1 / sqrt(mean + 1e-6)
 // is evaluated in binary64 and rounded once to binary32; the reference uses
 // an approximate rsqrt (src/kernels.rs:5-6), so `out` matches it within its
@@ -227,8 +227,18 @@ __global__ __launch_bounds__(256) void norm_quantize_4096(
     float a = part[t] + part[t + 128];           // d = 128 (t < 64)
     const float b = part[t + 64] + part[t + 192];  // d = 128 (t + 64 < 128)
     a = a + b;                                   // d = 64
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) a = a + __shfl_down(a, d, kWave);
+    // d = 32 .. 1: lane t adds lane t + d's partial, the same pairs as the
+    // reference's tree (lane 0 ends with the sum; the other lanes' values
+    // past each level are unused).  Cross-lane moves without LDS traffic:
+    // v_permlane32_swap (lanes 0-31 receive lanes 32-63), ds_swizzle
+    // xor 16, then DPP row_shl:8/4/2/1 inside each 16-lane row.
+    a = a + __int_as_float((int)__builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a),
+                                                                  false, false)[1]);
+    a = a + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(a), 0x401F));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x108, 0xF, 0xF, false));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x104, 0xF, 0xF, false));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x102, 0xF, 0xF, false));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x101, 0xF, 0xF, false));
     if (t == 0) {
       const float m = a / 4096.0f + 1e-6f;  // RN division, RN add
       inv_shared = (float)(1.0 / __builtin_sqrt((double)m));
