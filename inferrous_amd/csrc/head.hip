@@ -158,8 +158,15 @@ __global__ __launch_bounds__(kHeadThreads) void head_packed_kernel(
     // whole sum chain below the last branch and holds all 128 values live
     asm volatile("" : "+v"(sum));
   }
-#pragma unroll
-  for (int d = 16; d > 0; d >>= 1) sum = sum + __shfl_down(sum, d, 32);
+  // The row's half-wave tree, lane t adding lane t + d for d = 16 .. 1 (the
+  // reference's pairs; lane 0 of each half ends with the sum): ds_swizzle
+  // xor 16 inside each 32-lane half, then DPP row_shl:8/4/2/1 inside each
+  // 16-lane row -- no LDS traffic.
+  sum = sum + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(sum), 0x401F));
+  sum = sum + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x108, 0xF, 0xF, false));
+  sum = sum + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x104, 0xF, 0xF, false));
+  sum = sum + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x102, 0xF, 0xF, false));
+  sum = sum + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x101, 0xF, 0xF, false));
   if (lane == 0 && row < rows) out[row] = bf16_rne(sum);
 }
 
