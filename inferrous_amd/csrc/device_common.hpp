@@ -98,12 +98,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max(max(a, b), max(c, d));
 }
 
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
 // The 64-bit maximum keeps the cross-lane shuffle form.  Its users are the
 // fused selection's wave publish and its finalize: measured on MI355X, the
 // DPP form above made the 151,936 x 4096 head's fused-selection GEMV slower
