@@ -897,16 +897,22 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, int& tile, uint32_t& 
   return kt % splits == 0 && kt / splits >= 4;
 }
 
-// gemm_tall plan for 8 <= m <= 64 and 128 < m <= 256 (measured on MI355X
-// on the Qwen3-8B projection shapes at M = 16, 64 and 129): 96-column tiles
+// gemm_tall plan for 8 <= m <= 256 (measured on MI355X on the Qwen3-8B
+// projection shapes at M = 16, 64, 65, 100, 128 and 129): 96-column tiles
 // when they alone give about one tile per CU; otherwise split K four ways
 // (two when K is short), with 96- or 64-column tiles, to reach about one
-// workgroup per CU.  Returns false when neither applies (the gemm_dma or
-// gemm_skinny routes then run).  ma: the M tile (64, 160 or 256 rows).
+// workgroup per CU.  For 64 < m <= 128 only wide N and long K take it: one
+// 160-row tile streams the weights once where gemm_dma's two 64-row tiles
+// stream them twice (gate_up at M = 100 24.6-24.9 against 33.3-34.1 us,
+// down 20.7 against 23.3-23.5), while qkv and o at K = 4096 measured level
+// or faster on gemm_dma's split route.  Returns false when no plan applies
+// (the gemm_dma or gemm_skinny routes then run).  ma: the M tile (64, 160 or
+// 256 rows).
 static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits, int& ma) {
-  if (m < 8 || (m > 64 && m <= 128) || m > 256 || k % 128 != 0) return false;
+  if (m < 8 || m > 256 || k % 128 != 0) return false;
   ma = m <= 64 ? 64 : m <= 160 ? 160 : 256;
   const uint32_t kt = k / 128, t96 = (n + 95) / 96;
+  if (m > 64 && m <= 128 && t96 < 224 && k < 8192) return false;
   if (t96 >= 224) {
     bn = 96;
     splits = 1;
@@ -1004,7 +1010,7 @@ static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   if (a.m == 0 || a.n == 0) return hipSuccess;
   const unsigned nb16 = (a.n + 15) / 16;
-  // 8 <= m <= 64 and 128 < m <= 256 go to gemm_tall when its plan applies.
+  // 8 <= m <= 256 goes to gemm_tall when its plan applies.
   // Otherwise, for small m: from m = 8 the 8-wave kernel with 64-row tiles
   // streams the weights faster when n gives at least 128 tiles; below that
   // the skinny kernel's split-K keeps more CUs busy.

@@ -581,7 +581,8 @@ def test_errors_raise_not_fall_back(env):
 # ------------------------------------------------------------------ split-K workspace
 @pytest.mark.parametrize("m,n,k", [(129, 4096, 12288), (512, 4096, 12288), (129, 4096, 4096), (129, 6144, 4096),
                                    (16, 4096, 12288), (64, 4096, 12288), (40, 6144, 4096),
-                                   (100, 96, 12288), (255, 1024, 4096),
+                                   (100, 96, 12288), (255, 1024, 4096), (100, 4096, 12288), (65, 4100, 12288),
+                                   (128, 4096, 4096),
                                    (129, 4100, 4096), (64, 4100, 12288), (512, 4100, 12288)])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
@@ -724,10 +725,10 @@ def test_linear_split_k_unaligned_outputs(env):
     assert np.array_equal(comb.to_host_vec(s)[1:], want_comb)
 
 
-@pytest.mark.parametrize("m", [8, 33, 64, 129, 193, 256])
+@pytest.mark.parametrize("m", [8, 33, 64, 65, 100, 128, 129, 193, 256])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_one_m_tile_wide_n(env, m, dtype, res):
-    """8 <= M <= 64 and 128 < M <= 256 on a wide N (the gate_up regime): one M tile,
+    """8 <= M <= 256 on a wide N (the gate_up regime): one M tile,
     waves past M idle, activation rows past M never loaded, a ragged last
     column tile; bit-exact against the oracle with and without a workspace."""
     from inferrous_amd import _lib
