@@ -31,8 +31,8 @@
 //    Workgroups are numbered XCD-aware (below).  Tile shape per problem is
 //    chosen by the host from the tile count.  With a caller workspace, some
 //    shapes run split-K (i32 slabs + splitk_epilogue).
-//  * gemm_tall (8 <= M <= 64 and 128 < M <= 256, k % 128 == 0; M tiles of
-//    64, 160 or 256 rows): one M tile holds every
+//  * gemm_tall (8 <= M <= 256, k % 128 == 0, where its plan applies; M tiles
+//    of 64, 160 or 256 rows): one M tile holds every
 //    activation row, so each weight tile streams from HBM once; the eight
 //    waves are stacked along M and those past M only move data; activation
 //    rows past M are never loaded; split-K on narrow n.
@@ -49,6 +49,7 @@
 //    (workgroup id mod 8 picks the XCD), so the panel is fetched into that
 //    XCD's L2 once.
 #include <algorithm>
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "internal.hpp"
@@ -249,8 +250,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Epilogue modes, resolved at compile time so the unrolled store loop stays
 // branch-free: raw accumulators, f32 or BF16 outputs, each optionally with
-// the residual sum bf(residual + out).
-enum { EP_I32 = 0, EP_F32 = 1, EP_BF16 = 2, EP_F32_RES = 3, EP_BF16_RES = 4 };
+// the residual sum bf(residual + out).  EP_SLAB is EP_I32 for a split-K slab
+// that is streamed: non-temporal stores, read back once by the slab epilogue.
+enum { EP_I32 = 0, EP_F32 = 1, EP_BF16 = 2, EP_F32_RES = 3, EP_BF16_RES = 4, EP_SLAB = 5 };
+constexpr bool raw_i32(int ep) { return ep == EP_I32 || ep == EP_SLAB; }
 
 // Epilogue of a wave's FM x FN grid of 32x32 accumulator blocks whose top
 // left corner is (row0, col0).  Lane l, value v of block (i, j) is row
@@ -268,7 +271,7 @@ __device__ __forceinline__ void store_blocks(const GemmArgs& a, const v16i (&acc
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int v = 0; v < 16; ++v) rows[i][v] = row0 + 32 * i + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-  if (EP == EP_I32) {
+  if (raw_i32(EP)) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const uint32_t c = col0 + 32 * j + (lane & 31);
@@ -276,8 +279,11 @@ __device__ __forceinline__ void store_blocks(const GemmArgs& a, const v16i (&acc
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          if (rows[i][v] < a.m && c < a.n)
-            reinterpret_cast<int32_t*>(a.out)[(size_t)rows[i][v] * a.n + c] = acc[i][j][v];
+          if (rows[i][v] < a.m && c < a.n) {
+            int32_t* o = reinterpret_cast<int32_t*>(a.out) + (size_t)rows[i][v] * a.n + c;
+            if (EP == EP_SLAB) __builtin_nontemporal_store(acc[i][j][v], o);
+            else *o = acc[i][j][v];
+          }
     }
     return;
   }
@@ -361,7 +367,7 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   int8_t* const ldsA = lds;
   int8_t* const ldsB = lds + SA * ASL;
 
-  // Split-K (splits > 1, EP_I32 only): workgroup (tile, split) sums K range
+  // Split-K (splits > 1, EP_SLAB or EP_I32): workgroup (tile, split) sums K range
   // [split * K / splits, (split + 1) * K / splits) into i32 slab `split` of
   // a.out; a separate epilogue kernel adds the slabs (exact) and dequantizes.
   const uint32_t T = tiles_m * tiles_n, G = T * splits;
@@ -375,7 +381,7 @@ __global__ __launch_bounds__(512) void gemm_dma(GemmArgs a, uint32_t tiles_m, ui
   const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
   const uint32_t K = a.k, KT = K / 128 / splits;
   const size_t kbase = (size_t)split * KT * 128;
-  if (EP == EP_I32) a.out = reinterpret_cast<int32_t*>(a.out) + (size_t)split * a.m * a.n;
+  if (raw_i32(EP)) a.out = reinterpret_cast<int32_t*>(a.out) + (size_t)split * a.m * a.n;
 
   // Sources of this wave's DMA loads (8 rows each); rows past M / N re-read
   // row 0 (their products only reach accumulator cells that are never
@@ -616,7 +622,7 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const uint32_t K = a.k, KT = K / 128 / splits;
   const size_t kbase = (size_t)split * KT * 128;
-  if (EP == EP_I32) a.out = reinterpret_cast<int32_t*>(a.out) + (size_t)split * a.m * a.n;
+  if (raw_i32(EP)) a.out = reinterpret_cast<int32_t*>(a.out) + (size_t)split * a.m * a.n;
 
   // This wave's DMA instructions: activation row groups w, w + 8, ... below
   // ceil(M / 8), weight row groups w, w + 8, ... below BN / 8.  Lane l fills
@@ -740,11 +746,18 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
 
 constexpr uint32_t kMaxSplits = 4;  // split-K plans use 2 or 4 slabs
 
+// A slab quad; NT: the slabs were streamed (EP_SLAB) and are read once.
+template <bool NT>
+__device__ __forceinline__ v4i load_slab(const int32_t* p) {
+  if (NT) return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+  return *reinterpret_cast<const v4i*>(p);
+}
+
 // Split-K epilogue: out[r][c] = epilogue(sum over slabs of partials[s][r][c]).
 // The i32 sum is exact in any order.  blockIdx.y walks rows (the row scale is
 // one scalar load), each thread four consecutive columns (n % 4 == 0), so the
 // slab, weight-scale and residual loads are all issued up front.
-template <int EP>
+template <int EP, bool NT>
 __global__ __launch_bounds__(256) void splitk_epilogue(GemmArgs a, const int32_t* __restrict__ partials,
                                                         uint32_t splits) {
   constexpr bool RES = EP == EP_F32_RES || EP == EP_BF16_RES;
@@ -763,7 +776,7 @@ __global__ __launch_bounds__(256) void splitk_epilogue(GemmArgs a, const int32_t
     v4i part[kMaxSplits];
 #pragma unroll
     for (uint32_t s = 0; s < kMaxSplits; ++s)
-      part[s] = *reinterpret_cast<const v4i*>(partials + min(s, splits - 1) * mn + i);
+      part[s] = load_slab<NT>(partials + min(s, splits - 1) * mn + i);
     const float asc = EP != EP_I32 ? a.asc[r] : 0.f;
     float res[4] = {0.f, 0.f, 0.f, 0.f};
     if (RES)
@@ -797,7 +810,7 @@ __global__ __launch_bounds__(256) void splitk_epilogue(GemmArgs a, const int32_t
 // aligned scales, residuals and outputs: every operand moves in 16-byte
 // loads and stores (one store of 8 BF16 values), so a row costs a quarter of
 // the 4-column kernel's store instructions.
-template <int EP>
+template <int EP, bool NT>
 __global__ __launch_bounds__(256) void splitk_epilogue8(GemmArgs a, const int32_t* __restrict__ partials,
                                                          uint32_t splits) {
   constexpr bool RES = EP == EP_F32_RES || EP == EP_BF16_RES;
@@ -822,8 +835,8 @@ __global__ __launch_bounds__(256) void splitk_epilogue8(GemmArgs a, const int32_
 #pragma unroll
     for (uint32_t s = 0; s < kMaxSplits; ++s) {
       const int32_t* ps = partials + min(s, splits - 1) * mn + i;
-      p0[s] = *reinterpret_cast<const v4i*>(ps);
-      p1[s] = *reinterpret_cast<const v4i*>(ps + 4);
+      p0[s] = load_slab<NT>(ps);
+      p1[s] = load_slab<NT>(ps + 4);
     }
     const float asc = EP != EP_I32 ? a.asc[r] : 0.f;
     v4i r0 = {0, 0, 0, 0}, r1 = {0, 0, 0, 0};
@@ -936,17 +949,35 @@ size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-template <int EP>
+// gemm_tall's split-K slab sets of at least this many bytes are streamed:
+// written with non-temporal stores (EP_SLAB) and read back non-temporally.
+// Measured on MI355X (graphs of 16 distinct-weight launches, GEMM + slab
+// epilogue, plain -> streamed): qkv at M = 255 23.6 -> 19.7-20.2 us, o at
+// M = 255 19.1 -> 15.9, down at M = 200 26.3 -> 25.1, qkv at M = 129
+// 19.4 -> 16.0, o at M = 129 14.4 -> 13.8-14.1, qkv at M = 40 13.6 -> 12.9.
+// The streamed GEMM itself runs 1.2-1.3 us faster (no dirty slab lines left
+// in L2 at its end).  Smaller sets, whose epilogue is latency-bound, lose
+// (down at M = 32, 2 MiB: 16.6 -> 17.0; at M = 16, 1 MiB: 15.4 -> 15.9), and
+// so does gemm_dma's split route (down at M = 512 38.3 -> 41.0, at M = 300
+// 32.0 -> 33.2): both keep the default policy.
+constexpr size_t kSlabStreamBytes = size_t(3) << 20;
+
+static bool stream_slabs(const GemmArgs& a, uint32_t splits) {
+  return (size_t)splits * a.m * a.n * sizeof(int32_t) >= kSlabStreamBytes;
+}
+
+template <int EP, bool NT>
 static void launch_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits, bool wide) {
   const uint32_t rows = std::min<uint32_t>(a.m, 65535);
   if (wide)
-    hipLaunchKernelGGL(splitk_epilogue8<EP>, dim3((a.n / 8 + 255) / 256, rows), dim3(256), 0, st, a, a.partials,
-                       splits);
+    hipLaunchKernelGGL((splitk_epilogue8<EP, NT>), dim3((a.n / 8 + 255) / 256, rows), dim3(256), 0, st, a,
+                       a.partials, splits);
   else
-    hipLaunchKernelGGL(splitk_epilogue<EP>, dim3((a.n / 4 + 255) / 256, rows), dim3(256), 0, st, a, a.partials,
-                       splits);
+    hipLaunchKernelGGL((splitk_epilogue<EP, NT>), dim3((a.n / 4 + 255) / 256, rows), dim3(256), 0, st, a,
+                       a.partials, splits);
 }
 
+template <bool NT>
 static hipError_t launch_splitk_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits) {
   if (splits < 1 || splits > kMaxSplits) return hipErrorInvalidValue;
   // 8 columns per thread when every row of every operand starts 16-byte
@@ -955,44 +986,50 @@ static hipError_t launch_splitk_epilogue(hipStream_t st, const GemmArgs& a, uint
                     (a.out_dtype == W8A8_OUT_I32 || aligned16(a.ws)) &&
                     (!a.residual || (aligned16(a.residual) && aligned16(a.combined)));
   if (a.out_dtype == W8A8_OUT_I32)
-    launch_epilogue<EP_I32>(st, a, splits, wide);
+    launch_epilogue<EP_I32, NT>(st, a, splits, wide);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    launch_epilogue<EP_F32_RES>(st, a, splits, wide);
+    launch_epilogue<EP_F32_RES, NT>(st, a, splits, wide);
   else if (a.out_dtype == W8A8_OUT_F32)
-    launch_epilogue<EP_F32>(st, a, splits, wide);
+    launch_epilogue<EP_F32, NT>(st, a, splits, wide);
   else if (a.residual)
-    launch_epilogue<EP_BF16_RES>(st, a, splits, wide);
+    launch_epilogue<EP_BF16_RES, NT>(st, a, splits, wide);
   else
-    launch_epilogue<EP_BF16>(st, a, splits, wide);
+    launch_epilogue<EP_BF16, NT>(st, a, splits, wide);
   return hipGetLastError();
+}
+
+// Split-K launch: `gemm` launches the split GEMM into a.partials, given the
+// slab mode as a compile-time constant; the slab epilogue follows.  Both
+// take the same slab policy (nt: streamed).
+template <typename Launch>
+static hipError_t launch_slabs(hipStream_t st, const GemmArgs& a, uint32_t splits, bool nt, Launch gemm) {
+  GemmArgs p = a;
+  p.out = a.partials;
+  p.out_dtype = W8A8_OUT_I32;
+  if (nt) gemm(std::integral_constant<int, EP_SLAB>{}, p);
+  else gemm(std::integral_constant<int, EP_I32>{}, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return nt ? launch_splitk_epilogue<true>(st, a, splits) : launch_splitk_epilogue<false>(st, a, splits);
 }
 
 template <int BM, int BN, int WM, int WN, int SA, int SB>
 static hipError_t launch_split(hipStream_t st, const GemmArgs& a, uint32_t splits) {
   const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
-  GemmArgs p = a;
-  p.out = a.partials;
-  p.out_dtype = W8A8_OUT_I32;
-  hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, EP_I32, false>), dim3(tm * tn * splits), dim3(512), 0, st, p,
-                     tm, tn, splits);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return launch_splitk_epilogue(st, a, splits);
+  return launch_slabs(st, a, splits, false, [&](auto ep, const GemmArgs& p) {
+    hipLaunchKernelGGL((gemm_dma<BM, BN, WM, WN, SA, SB, decltype(ep)::value, false>), dim3(tm * tn * splits),
+                       dim3(512), 0, st, p, tm, tn, splits);
+  });
 }
 
 template <int BN, int SA, int SB, int MA>
 static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits) {
   const uint32_t tn = (a.n + BN - 1) / BN;
   const dim3 grid(tn * splits), block(512);
-  if (splits > 1) {
-    GemmArgs p = a;
-    p.out = a.partials;
-    p.out_dtype = W8A8_OUT_I32;
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32, false>), grid, block, 0, st, p, tn, splits);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    return launch_splitk_epilogue(st, a, splits);
-  }
+  if (splits > 1)
+    return launch_slabs(st, a, splits, stream_slabs(a, splits), [&](auto ep, const GemmArgs& p) {
+      hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, decltype(ep)::value, false>), grid, block, 0, st, p, tn, splits);
+    });
   if (a.out_dtype == W8A8_OUT_I32)
     hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32, kRotateK>), grid, block, 0, st, a, tn, 1u);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)

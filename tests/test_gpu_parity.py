@@ -583,12 +583,18 @@ def test_errors_raise_not_fall_back(env):
                                    (16, 4096, 12288), (64, 4096, 12288), (40, 6144, 4096),
                                    (100, 96, 12288), (255, 1024, 4096), (100, 4096, 12288), (65, 4100, 12288),
                                    (128, 4096, 4096),
-                                   (129, 4100, 4096), (64, 4100, 12288), (512, 4100, 12288)])
+                                   (129, 4100, 4096), (64, 4100, 12288), (512, 4100, 12288),
+                                   (16, 4100, 12288), (100, 1024, 4096)])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     """w8a8_linear_ex with a workspace (split-K partials + exact i32 epilogue)
     equals the call without one and the oracle, bit for bit -- also on a
-    second call with the same workspace, which carries nothing between calls."""
+    second call with the same workspace, which carries nothing between calls.
+    The shapes cover both slab policies with the 16-byte and the 4-column
+    epilogue each: streamed (gemm_tall from 3 MiB of slabs, e.g. 129 x 4096 x
+    4096 and 64 x 4100 x 12288) and plain (smaller gemm_tall sets such as
+    16 x 4100 x 12288 and 100 x 96 x 12288, and every gemm_dma split such as
+    512 x 4100 x 12288 and 100 x 1024 x 4096)."""
     from inferrous_amd import _lib
     ctx, mod, s = env
     print(f"split-K m={m} n={n} k={k} {np.dtype(dtype).name} res={res}", flush=True)
