@@ -892,40 +892,32 @@ __global__ __launch_bounds__(256) void splitk_epilogue8(GemmArgs a, const int32_
   }
 }
 
-// Split-K plan, measured on MI355X: the K = 12288 down projection (few,
-// long tiles) and the M <= 255 shapes with at most 128 tiles of 128 x 64.
-// tile 0 = 128 x 128, 1 = 128 x 64.
-static bool split_plan(uint32_t m, uint32_t n, uint32_t k, int& tile, uint32_t& splits) {
-  if (m <= 64 || k % 128 != 0 || n % 4 != 0) return false;
+// gemm_dma's split-K plan (128 x 128 tiles, two slabs): M > 256 at K >= 8192,
+// the down projection's few, long tiles (measured on MI355X at M = 300 and
+// 512).  gemm_tall's plan covers M <= 256.
+static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
+  if (m <= 256 || k < 8192 || k % 128 != 0 || n % 4 != 0) return false;
   const uint32_t kt = k / 128;
-  if (k >= 8192) {
-    tile = 0;
-    splits = m >= 256 ? 2 : 4;
-  } else if (m < 256 && (uint64_t)((m + 127) / 128) * ((n + 63) / 64) <= 128) {
-    tile = 1;
-    splits = 2;
-  } else {
-    return false;
-  }
+  splits = 2;
   return kt % splits == 0 && kt / splits >= 4;
 }
 
 // gemm_tall plan for 8 <= m <= 256 (measured on MI355X on the Qwen3-8B
-// projection shapes at M = 16, 64, 65, 100, 128 and 129): 96-column tiles
-// when they alone give about one tile per CU; otherwise split K four ways
-// (two when K is short), with 96- or 64-column tiles, to reach about one
-// workgroup per CU.  For 64 < m <= 128 only wide N and long K take it: one
-// 160-row tile streams the weights once where gemm_dma's two 64-row tiles
-// stream them twice (gate_up at M = 100 24.6-24.9 against 33.3-34.1 us,
-// down 20.7 against 23.3-23.5), while qkv and o at K = 4096 measured level
-// or faster on gemm_dma's split route.  Returns false when no plan applies
-// (the gemm_dma or gemm_skinny routes then run).  ma: the M tile (64, 160 or
-// 256 rows).
+// projection shapes at M = 16, 64, 65, 80, 100, 128 and 129): 96-column
+// tiles when they alone give about one tile per CU; otherwise split K four
+// ways (two when K is short), with 96- or 64-column tiles, to reach about one
+// workgroup per CU.  For 64 < m <= 128 one 160-row tile streams the weights
+// once where gemm_dma's two 64-row tiles stream them twice (gate_up at
+// M = 100 24.6-24.9 against 33.3-34.1 us, down 20.7 against 23.3-23.5), and
+// with streamed slabs the split route also beats gemm_dma's split-K 2 on
+// qkv and o (qkv at M = 65 / 100 / 128 12.6 / 14.1 / 14.5 against
+// 13.2-13.3 / 14.6 / 15.5, o 10.9 / 11.6 / 12.7 against 12.0 / 12.7 / 13.2).
+// Returns false when no plan applies (the gemm_dma or gemm_skinny routes
+// then run).  ma: the M tile (64, 160 or 256 rows).
 static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits, int& ma) {
   if (m < 8 || m > 256 || k % 128 != 0) return false;
   ma = m <= 64 ? 64 : m <= 160 ? 160 : 256;
   const uint32_t kt = k / 128, t96 = (n + 95) / 96;
-  if (m > 64 && m <= 128 && t96 < 224 && k < 8192) return false;
   if (t96 >= 224) {
     bn = 96;
     splits = 1;
@@ -943,7 +935,7 @@ size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
   uint32_t splits;
   int ma;
   if (tall_plan(m, n, k, tile, splits, ma)) return splits > 1 ? (size_t)splits * m * n * sizeof(int32_t) : 0;
-  if (!split_plan(m, n, k, tile, splits)) return 0;
+  if (!split_plan(m, n, k, splits)) return 0;
   return (size_t)splits * m * n * sizeof(int32_t);
 }
 
@@ -1071,12 +1063,10 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   } else if (a.m <= 64 && !wide) {
     hipLaunchKernelGGL((gemm_skinny<4, 4, 2>), dim3(nb16, 1), dim3(256), 0, st, a);
   } else if (a.k % 128 == 0) {
-    int tile;
     uint32_t splits;
-    if (a.partials && split_plan(a.m, a.n, a.k, tile, splits) &&
+    if (a.partials && split_plan(a.m, a.n, a.k, splits) &&
         a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))
-      return tile == 0 ? launch_split<128, 128, 32, 64, 4, 4>(st, a, splits)
-                       : launch_split<128, 64, 32, 32, 4, 4>(st, a, splits);
+      return launch_split<128, 128, 32, 64, 4, 4>(st, a, splits);
     // Tile per problem, measured on MI355X at M = 129 / 512 on the Qwen3-8B
     // projection shapes: the largest tile that still gives about one tile
     // per CU, smaller tiles for narrow N.

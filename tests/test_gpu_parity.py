@@ -593,8 +593,8 @@ def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     The shapes cover both slab policies with the 16-byte and the 4-column
     epilogue each: streamed (gemm_tall from 3 MiB of slabs, e.g. 129 x 4096 x
     4096 and 64 x 4100 x 12288) and plain (smaller gemm_tall sets such as
-    16 x 4100 x 12288 and 100 x 96 x 12288, and every gemm_dma split such as
-    512 x 4100 x 12288 and 100 x 1024 x 4096)."""
+    16 x 4100 x 12288, 100 x 96 x 12288 and 100 x 1024 x 4096, and gemm_dma's
+    split route above M = 256: 512 x 4096 x 12288 and 512 x 4100 x 12288)."""
     from inferrous_amd import _lib
     ctx, mod, s = env
     print(f"split-K m={m} n={n} k={k} {np.dtype(dtype).name} res={res}", flush=True)
