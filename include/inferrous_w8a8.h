@@ -272,6 +272,39 @@ int w8a8_linear_swiglu_quantize(void *stream, const int8_t *q, const float *asc,
                                 int8_t *q_out, float *scales_out,
                                 int out_dtype);
 
+/* norm_quantize of one 4096-wide f32 row (as w8a8_norm_quantize with
+ * rows = 1) followed by linear (residual == NULL) or linear_residual of its
+ * codes at M = 1, in one launch.  No counterpart in the reference, which
+ * runs the two kernels (src/gpu.rs:552 then the projection at :565-590).
+ * Every workgroup of the GEMV recomputes the row's codes and scale with the
+ * producer's arithmetic and order; workgroup 0 also writes them.  Results
+ * are bit-identical to the two calls:
+ *   q[4096] (16-byte aligned), scale[1];
+ *   maxima[0] reset to bits(1e-8f) when maxima is not NULL;
+ *   out_norm[4096], the normalised row, when out_norm is not NULL;
+ *   out[n], and combined[n] with residual[n], as w8a8_linear /
+ *   w8a8_linear_residual write them for w[n, 4096], ws[n].
+ * n >= 1.  out_dtype is F32 or BF16, or I32 without a residual.  x and gain
+ * must not overlap any output. */
+int w8a8_norm_quantize_linear(void *stream, const float *x,
+                              const float *gain, float *out_norm, int8_t *q,
+                              float *scale, uint32_t *maxima,
+                              const int8_t *w, const float *ws, size_t n,
+                              const float *residual, void *out,
+                              void *combined, int out_dtype);
+
+/* quantize of one f32 row of width 4096 (as w8a8_quantize with rows = 1)
+ * followed by linear or linear_residual of its codes at M = 1, in one
+ * launch: the reference's host linear_residual at decode (src/gpu.rs:364-415:
+ * quantize at :397, then the kernel at :402-415) as one kernel.  Outputs
+ * and rules as for w8a8_norm_quantize_linear (maxima_reset as w8a8_quantize's
+ * maxima_reset); width must be 4096. */
+int w8a8_quantize_linear(void *stream, const float *x, uint32_t width,
+                         int8_t *q, float *scale, uint32_t *maxima_reset,
+                         const int8_t *w, const float *ws, size_t n,
+                         const float *residual, void *out, void *combined,
+                         int out_dtype);
+
 /* `swiglu` (src/kernels.rs:2172-2190): act = as above, elementwise over
  * gate/up [rows, width] in dtype (F32 or BF16); maxima as above, per row
  * (the reference publishes only for its single 12288-wide decode row). */

@@ -655,6 +655,72 @@ int w8a8_linear_swiglu_quantize(void* stream, const int8_t* q, const float* asc,
                     scales_out, out_dtype);
 }
 
+namespace {
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  if (!a || !b) return false;
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+// The producer (norm_quantize when gain is set, quantize otherwise) of one
+// 4096-wide row and the M = 1 linear on its codes, in one launch.
+int produce_linear(void* stream, const float* x, const float* gain, float* out_norm, int8_t* q, float* scale,
+                   uint32_t* maxima, const int8_t* w, const float* ws, size_t n, const float* residual, void* out,
+                   void* combined, int out_dtype) {
+  if (!valid_dtype(out_dtype) || (residual && out_dtype == W8A8_OUT_I32)) return W8A8_EARG;
+  if (n == 0 || n > kU32Max) return W8A8_ESHAPE;
+  if (!x || !q || !scale || !w || !ws || !out) return W8A8_ENULL;
+  if ((residual == nullptr) != (combined == nullptr)) return W8A8_ENULL;
+  if (!al(x, 4) || !al(gain, 4) || !al(out_norm, 4) || !al(q, 16) || !al(scale, 4) || !al(maxima, 4) ||
+      !al(w, 16) || !al(ws, 4) || !al(out, out_align(out_dtype)) || !al(residual, 4) ||
+      !al(combined, out_align(out_dtype)))
+    return W8A8_EALIGN;
+  // Every workgroup reads the row (and the gains) while workgroup 0 and the
+  // GEMV write the outputs, so no output may share their bytes.
+  const size_t ob = n * (size_t)out_align(out_dtype);
+  const struct {
+    const void* p;
+    size_t bytes;
+  } outs[] = {{out_norm, 4096 * 4}, {q, 4096}, {scale, 4}, {maxima, 4}, {out, ob}, {combined, ob}};
+  for (const auto& o : outs)
+    if (overlaps(x, 4096 * 4, o.p, o.bytes) || overlaps(gain, 4096 * 4, o.p, o.bytes)) return W8A8_EARG;
+  if (!ready()) return W8A8_EINIT;
+  ProduceArgs p{};
+  p.x = x;
+  p.gain = gain;
+  p.normed = out_norm;
+  p.q = q;
+  p.scale = scale;
+  p.maxima = maxima;
+  p.w = w;
+  p.ws = ws;
+  p.n = (uint32_t)n;
+  p.residual = residual;
+  p.out = out;
+  p.combined = combined;
+  p.out_dtype = out_dtype;
+  return hip_status(launch_gemv_produce((hipStream_t)stream, p));
+}
+
+}  // namespace
+
+int w8a8_norm_quantize_linear(void* stream, const float* x, const float* gain, float* out_norm, int8_t* q,
+                              float* scale, uint32_t* maxima, const int8_t* w, const float* ws, size_t n,
+                              const float* residual, void* out, void* combined, int out_dtype) {
+  if (!gain) return W8A8_ENULL;
+  return produce_linear(stream, x, gain, out_norm, q, scale, maxima, w, ws, n, residual, out, combined,
+                        out_dtype);
+}
+
+int w8a8_quantize_linear(void* stream, const float* x, uint32_t width, int8_t* q, float* scale,
+                         uint32_t* maxima_reset, const int8_t* w, const float* ws, size_t n,
+                         const float* residual, void* out, void* combined, int out_dtype) {
+  if (width != 4096) return W8A8_ESHAPE;
+  return produce_linear(stream, x, nullptr, nullptr, q, scale, maxima_reset, w, ws, n, residual, out, combined,
+                        out_dtype);
+}
+
 size_t w8a8_select_workspace_bytes(size_t n) {
   (void)n;
   return kSelectBlocks * sizeof(uint64_t);

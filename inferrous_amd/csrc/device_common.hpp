@@ -98,6 +98,56 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max(max(a, b), max(c, d));
 }
 
+// Maximum over a 256-thread workgroup (every thread active): the wave maxima,
+// then one LDS round through red[4].  The quantizers' row maximum.
+__device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
+  m = wave_max_u32(m);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+// RMSNorm scale of one 4096-wide row over a 256-thread workgroup, thread t
+// holding v[i] = x[t + 256 i] (i < 16).  The sum of squares keeps the
+// reference's order exactly (src/kernels.rs:509-538, the tree of `norm`
+// :354-392): thread t sums RN(x^2) over its coordinates (sequential RN
+// adds), then the halving tree p[t] = RN(p[t] + p[t + d]), d = 128, 64, ...,
+// 1 -- here the first two levels in one wave from LDS, the rest with
+// cross-lane moves with the same pairs (v_permlane32_swap: lanes 0-31
+// receive lanes 32-63; ds_swizzle xor 16; DPP row_shl 8/4/2/1 inside each
+// 16-lane row; lane 0 ends with the sum, the other lanes' values past each
+// level are unused).  inv = 1 / sqrt(mean + 1e-6) is evaluated in binary64
+// and rounded once to binary32; the reference uses an approximate rsqrt
+// (src/kernels.rs:5-6), so normalised values match it within its tolerance.
+// Returns inv to every thread, after the barrier that publishes it.
+__device__ __forceinline__ float norm_inv_4096(const float (&v)[16], float* part, float* inv) {
+  const int t = threadIdx.x;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s = s + v[i] * v[i];
+  part[t] = s;
+  __syncthreads();
+  if (t < 64) {
+    float a = part[t] + part[t + 128];           // d = 128 (t < 64)
+    const float b = part[t + 64] + part[t + 192];  // d = 128 (t + 64 < 128)
+    a = a + b;                                   // d = 64
+    a = a + __int_as_float((int)__builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a),
+                                                                  false, false)[1]);
+    a = a + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(a), 0x401F));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x108, 0xF, 0xF, false));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x104, 0xF, 0xF, false));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x102, 0xF, 0xF, false));
+    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x101, 0xF, 0xF, false));
+    if (t == 0) {
+      const float m = a / 4096.0f + 1e-6f;  // RN division, RN add
+      *inv = (float)(1.0 / __builtin_sqrt((double)m));
+    }
+  }
+  __syncthreads();
+  return *inv;
+}
+
 // The 64-bit maximum keeps the cross-lane shuffle form.  Its users are the
 // fused selection's wave publish and its finalize: measured on MI355X, the
 // DPP form above made the 151,936 x 4096 head's fused-selection GEMV slower

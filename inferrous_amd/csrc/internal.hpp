@@ -86,6 +86,26 @@ hipError_t launch_norm_quantize(hipStream_t st, const float* x, const float* gai
                                 float* out, int8_t* q, float* scales, uint32_t* maxima);  // width 4096
 
 hipError_t launch_gemv(hipStream_t st, GemvArgs& a);
+
+// A producer of one 4096-wide f32 row's codes -- norm_quantize when gain is
+// set, quantize otherwise -- and the M = 1 linear (or linear_residual) on
+// those codes, in one launch.
+struct ProduceArgs {
+  const float* x;
+  const float* gain;
+  float* normed;          // optional: norm_quantize's normalised row
+  int8_t* q;              // the row's codes (16-byte aligned)
+  float* scale;
+  uint32_t* maxima;       // optional: reset to the floor, as the producers do
+  const int8_t* w;
+  const float* ws;
+  uint32_t n;             // >= 1
+  const float* residual;  // with combined: linear_residual
+  void* out;
+  void* combined;
+  int out_dtype;
+};
+hipError_t launch_gemv_produce(hipStream_t st, const ProduceArgs& p);
 // Diagnostics: the one-matrix M = 1 GEMV with per-wave clock stamps.
 size_t gemv_timeline_waves(size_t n, uint32_t k);
 hipError_t launch_gemv_timeline(hipStream_t st, const int8_t* q, const float* asc, const int8_t* w,

@@ -20,14 +20,6 @@ namespace w8a8 {
 
 constexpr int kQThreads = 256;
 
-__device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
-  m = wave_max_u32(m);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  return max(max(red[0], red[1]), max(red[2], red[3]));
-}
-
 // f32 rows, width % 4 == 0, 16-byte aligned rows.  NV = float4 per thread
 // held in registers (NV * 256 * 4 >= width), or 0: the row is streamed
 // twice (the second pass hits L2).  The NV loads are issued unconditionally
@@ -194,15 +186,10 @@ __global__ __launch_bounds__(256) void rounding_probe_kernel(const float* __rest
 }
 
 // ------------------------------------------------------------------ launchers
-// RMSNorm of one 4096-wide row per workgroup, then the row's quantization.
-// The sum of squares keeps the reference's order exactly: thread t sums
-// RN(x^2) over coordinates t + 256 i (i = 0..15, sequential RN adds), then
-// the halving tree p[t] = RN(p[t] + p[t + d]), d = 128, 64, ..., 1 -- here
-// the first two levels in one wave from LDS, the rest with cross-lane moves
-// (lane 0 only consumes in-range partners).  inv = 1 / sqrt(mean + 1e-6)
-// is evaluated in binary64 and rounded once to binary32; the reference uses
-// an approximate rsqrt (src/kernels.rs:5-6), so `out` matches it within its
-// tolerance, while (q, scale) are exactly the quantization of `out`.
+// RMSNorm of one 4096-wide row per workgroup (norm_inv_4096: the
+// reference's sum order), then the row's quantization.  `out` matches the
+// reference within its tolerance, while (q, scale) are exactly the
+// quantization of `out`.
 __global__ __launch_bounds__(256) void norm_quantize_4096(
     const float* __restrict__ x, const float* __restrict__ gain, float* __restrict__ out,
     int8_t* __restrict__ q, float* __restrict__ scales, uint32_t* __restrict__ maxima) {
@@ -218,34 +205,7 @@ __global__ __launch_bounds__(256) void norm_quantize_4096(
     v[i] = row[t + 256 * i];
     g[i] = gain[t + 256 * i];
   }
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s = s + v[i] * v[i];
-  part[t] = s;
-  __syncthreads();
-  if (t < 64) {
-    float a = part[t] + part[t + 128];           // d = 128 (t < 64)
-    const float b = part[t + 64] + part[t + 192];  // d = 128 (t + 64 < 128)
-    a = a + b;                                   // d = 64
-    // d = 32 .. 1: lane t adds lane t + d's partial, the same pairs as the
-    // reference's tree (lane 0 ends with the sum; the other lanes' values
-    // past each level are unused).  Cross-lane moves without LDS traffic:
-    // v_permlane32_swap (lanes 0-31 receive lanes 32-63), ds_swizzle
-    // xor 16, then DPP row_shl:8/4/2/1 inside each 16-lane row.
-    a = a + __int_as_float((int)__builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a),
-                                                                  false, false)[1]);
-    a = a + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(a), 0x401F));
-    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x108, 0xF, 0xF, false));
-    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x104, 0xF, 0xF, false));
-    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x102, 0xF, 0xF, false));
-    a = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x101, 0xF, 0xF, false));
-    if (t == 0) {
-      const float m = a / 4096.0f + 1e-6f;  // RN division, RN add
-      inv_shared = (float)(1.0 / __builtin_sqrt((double)m));
-    }
-  }
-  __syncthreads();
-  const float inv = inv_shared;
+  const float inv = norm_inv_4096(v, part, &inv_shared);
   float* orow = out + r * 4096;
   uint32_t mb = kFloorBits;
 #pragma unroll

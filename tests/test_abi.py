@@ -131,6 +131,50 @@ def test_diag_timeline_validation_precedes_device():
 
 
 @pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_producer_linear_validation_precedes_device():
+    """w8a8_norm_quantize_linear / w8a8_quantize_linear reject malformed
+    calls on the host, including any output that shares bytes with the row
+    every workgroup reads."""
+    L = _lib.lib()
+    B = A + 0x100000  # outputs, clear of x [A, A + 16 KiB) and gain [A + 16 KiB, A + 32 KiB)
+
+    def nql(**kw):
+        a = dict(x=A, gain=A + 0x4000, norm=B, q=B + 0x8000, sc=B + 0x9000, mx=B + 0x9010, w=B + 0x10000,
+                 ws=B + 0x20000, n=4096, res=None, out=B + 0x30000, comb=None, dt=_lib.OUT_BF16)
+        a.update(kw)
+        return L.w8a8_norm_quantize_linear(None, a["x"], a["gain"], a["norm"], a["q"], a["sc"], a["mx"], a["w"],
+                                           a["ws"], a["n"], a["res"], a["out"], a["comb"], a["dt"])
+
+    def ql(**kw):
+        a = dict(x=A, width=4096, q=B + 0x8000, sc=B + 0x9000, mx=None, w=B + 0x10000, ws=B + 0x20000, n=4096,
+                 res=B + 0x40000, out=B + 0x30000, comb=B + 0x50000, dt=_lib.OUT_F32)
+        a.update(kw)
+        return L.w8a8_quantize_linear(None, a["x"], a["width"], a["q"], a["sc"], a["mx"], a["w"], a["ws"], a["n"],
+                                      a["res"], a["out"], a["comb"], a["dt"])
+
+    assert nql() == _lib.EINIT
+    assert nql(norm=None, mx=None) == _lib.EINIT
+    assert nql(n=0) == _lib.ESHAPE
+    assert nql(n=1 << 33) == _lib.ESHAPE
+    assert nql(gain=None) == _lib.ENULL
+    assert nql(q=None) == _lib.ENULL and nql(sc=None) == _lib.ENULL and nql(out=None) == _lib.ENULL
+    assert nql(res=B + 0x40000) == _lib.ENULL          # a residual needs combined
+    assert nql(q=B + 0x8004) == _lib.EALIGN            # codes are written 16 bytes at a time
+    assert nql(x=A + 2) == _lib.EALIGN
+    assert nql(dt=7) == _lib.EARG
+    assert nql(res=B + 0x40000, comb=B + 0x50000, dt=_lib.OUT_I32) == _lib.EARG
+    assert nql(norm=A + 0x10) == _lib.EARG             # the normalised row over x
+    assert nql(out=A + 0x4100) == _lib.EARG            # out over the gains
+    assert nql(q=A + 0x3ff0) == _lib.EARG              # codes over x's last bytes
+    assert ql() == _lib.EINIT
+    assert ql(res=None, comb=None) == _lib.EINIT
+    assert ql(width=4095) == _lib.ESHAPE and ql(width=12288) == _lib.ESHAPE
+    assert ql(q=None) == _lib.ENULL
+    assert ql(comb=None) == _lib.ENULL
+    assert ql(comb=A) == _lib.EARG                      # combined over x
+
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
 def test_linear_validation_precedes_device():
     assert lin() == _lib.EINIT                       # well formed: stops at init
     assert lin(k=4095) == _lib.ESHAPE                # k % 16
