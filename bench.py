@@ -221,8 +221,9 @@ def ragged_profile_run() -> int:
 def chain_profile_run() -> int:
     """Workload for a kernel-trace profile of the decode layer chain
     (src/gpu.rs:571-790 order) at M = 1: 8 layers of distinct weights, the
-    reference call sequence and the chain with linear_swiglu_quantize, each
-    captured once and replayed 5 times."""
+    reference call sequence, the chain with linear_swiglu_quantize, and that
+    chain with the qkv and o producers folded into their GEMVs, each captured
+    once and replayed 5 times."""
     from inferrous_amd import CudaContext, DeviceBuffer, Graph, load, synth
     ctx = CudaContext(0)
     mod = load(ctx)
@@ -253,31 +254,37 @@ def chain_profile_run() -> int:
     qkv, o, down = (DeviceBuffer.zeroed(s, n, np.uint16) for n in (6144, h, h))
     comb = DeviceBuffer.zeroed(s, h, np.uint16)
 
-    def chain(fused: bool):
+    def chain(mode: int):
+        # 0: the reference's calls; 1: linear_swiglu_quantize for the MLP
+        # pair; 2: as 1, with the qkv and o producers folded into their GEMVs
         for (mats, (wg_, sg_, wu_, su_)) in layers:
             (wqkv, sqkv), (wo, so), _, (wd, sd) = mats
-            mod.norm_quantize(s, None, x, gains[0], normed, q4, sc4, mx)
-            mod.linear(s, None, q4, sc4, wqkv, sqkv, h, qkv)
-            mod.quantize(s, None, x, h, q4, sc4)
-            mod.linear_residual(s, None, q4, sc4, wo, so, h, resid, o, comb)
+            if mode == 2:
+                mod.norm_quantize_linear(s, None, x, gains[0], normed, q4, sc4, mx, wqkv, sqkv, qkv)
+                mod.quantize_linear(s, None, x, q4, sc4, wo, so, o, resid, comb)
+            else:
+                mod.norm_quantize(s, None, x, gains[0], normed, q4, sc4, mx)
+                mod.linear(s, None, q4, sc4, wqkv, sqkv, h, qkv)
+                mod.quantize(s, None, x, h, q4, sc4)
+                mod.linear_residual(s, None, q4, sc4, wo, so, h, resid, o, comb)
             mod.norm_quantize(s, None, x, gains[1], normed, q4, sc4, mx)
-            if fused:
+            if mode >= 1:
                 mod.linear_swiglu_quantize(s, None, q4, sc4, h, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx, q12, sc12)
                 mod.linear_residual(s, None, q12, sc12, wd, sd, ffn, resid, down, comb)
             else:
                 mod.linear_swiglu(s, None, q4, sc4, h, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx)
                 mod.linear_quantize_with_max(s, None, act, ffn, mx, q12, sc12, wd, sd, down, resid, comb)
 
-    for fused in (False, True):
-        chain(fused)
+    for mode, label in ((0, "reference calls"), (1, "fused MLP tail"), (2, "fused producers")):
+        chain(mode)
         s.synchronize()
         g = Graph(s)
         with g:
-            chain(fused)
+            chain(mode)
         for _ in range(5):
             g.launch()
         s.synchronize()
-        print(f"chain profile ({'fused MLP tail' if fused else 'reference calls'}) done", flush=True)
+        print(f"chain profile ({label}) done", flush=True)
     return 0
 
 
@@ -590,13 +597,19 @@ def main() -> int:
                            DeviceBuffer.view_of(gw, ffn * 4096, ffn * 4096),
                            DeviceBuffer.view_of(gws, ffn, ffn)))
 
-        def layer_chain(fused_mlp: bool = False):
+        def layer_chain(fused_mlp: bool = False, fused_producers: bool = False):
             for mats, (wg_, sg_, wu_, su_) in zip(layers, halves):
                 (_, _, _, wqkv, sqkv), (_, _, _, wo, so), _, (_, _, _, wd, sd) = mats
-                mod.norm_quantize(s, None, xs[4096], gains[0], normed, q4, sc4, mx)
-                mod.linear(s, None, q4, sc4, wqkv, sqkv, 4096, outs["qkv"])
-                mod.quantize(s, None, xs[4096], 4096, q4, sc4)
-                mod.linear_residual(s, None, q4, sc4, wo, so, 4096, resid, outs["o"], comb)
+                if fused_producers:
+                    # norm_quantize + qkv and quantize + o, one launch each
+                    mod.norm_quantize_linear(s, None, xs[4096], gains[0], normed, q4, sc4, mx, wqkv, sqkv,
+                                             outs["qkv"])
+                    mod.quantize_linear(s, None, xs[4096], q4, sc4, wo, so, outs["o"], resid, comb)
+                else:
+                    mod.norm_quantize(s, None, xs[4096], gains[0], normed, q4, sc4, mx)
+                    mod.linear(s, None, q4, sc4, wqkv, sqkv, 4096, outs["qkv"])
+                    mod.quantize(s, None, xs[4096], 4096, q4, sc4)
+                    mod.linear_residual(s, None, q4, sc4, wo, so, 4096, resid, outs["o"], comb)
                 mod.norm_quantize(s, None, xs[4096], gains[1], normed, q4, sc4, mx)
                 if fused_mlp:
                     mod.linear_swiglu_quantize(s, None, q4, sc4, 4096, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx,
@@ -628,6 +641,16 @@ def main() -> int:
             "launches": 8 * synth.LAYERS + 3,
             "chain": "norm_quantize, qkv, quantize, o+residual, norm_quantize, linear_swiglu_quantize, down+residual; lm_head"}
         log(f"decode chain, fused MLP tail: {ms * 1e3:.1f} us ({extras['decode_chain_fused_mlp']['GB/s']} GB/s)")
+        # and with the qkv and o producers folded into their GEMVs
+        # (w8a8_norm_quantize_linear, w8a8_quantize_linear)
+        ms = time_graph(capture(lambda: layer_chain(fused_mlp=True, fused_producers=True)), 20)
+        extras["decode_chain_fused_producers"] = {
+            "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "launches": 6 * synth.LAYERS + 3,
+            "chain": "norm_quantize_linear (qkv), quantize_linear (o+residual), norm_quantize, "
+                     "linear_swiglu_quantize, down+residual; lm_head"}
+        log(f"decode chain, fused producers: {ms * 1e3:.1f} us "
+            f"({extras['decode_chain_fused_producers']['GB/s']} GB/s)")
         # latency-bound producers at M = 1: per call in a graph of 100
         # stream-ordered calls (launch gap included)
         act12 = DeviceBuffer.from_host(s, synth.normal_rows(45, 1, ffn).reshape(-1))
