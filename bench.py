@@ -256,12 +256,16 @@ def chain_profile_run() -> int:
 
     def chain(mode: int):
         # 0: the reference's calls; 1: linear_swiglu_quantize for the MLP
-        # pair; 2: as 1, with the qkv and o producers folded into their GEMVs
+        # pair; 2: every K = 4096 producer folded into its GEMV
         for (mats, (wg_, sg_, wu_, su_)) in layers:
             (wqkv, sqkv), (wo, so), _, (wd, sd) = mats
             if mode == 2:
                 mod.norm_quantize_linear(s, None, x, gains[0], normed, q4, sc4, mx, wqkv, sqkv, qkv)
                 mod.quantize_linear(s, None, x, q4, sc4, wo, so, o, resid, comb)
+                mod.norm_quantize_linear_swiglu(s, None, x, gains[1], normed, q4, sc4, wg_, sg_, gbuf, wu_, su_,
+                                                ubuf, act, mx, q12, sc12)
+                mod.linear_residual(s, None, q12, sc12, wd, sd, ffn, resid, down, comb)
+                continue
             else:
                 mod.norm_quantize(s, None, x, gains[0], normed, q4, sc4, mx)
                 mod.linear(s, None, q4, sc4, wqkv, sqkv, h, qkv)
@@ -610,6 +614,12 @@ def main() -> int:
                     mod.linear(s, None, q4, sc4, wqkv, sqkv, 4096, outs["qkv"])
                     mod.quantize(s, None, xs[4096], 4096, q4, sc4)
                     mod.linear_residual(s, None, q4, sc4, wo, so, 4096, resid, outs["o"], comb)
+                if fused_producers:
+                    # norm_quantize folded into the SwiGLU GEMV (+ its row tail)
+                    mod.norm_quantize_linear_swiglu(s, None, xs[4096], gains[1], normed, q4, sc4, wg_, sg_, gbuf,
+                                                    wu_, su_, ubuf, act, mx, q12, sc12)
+                    mod.linear_residual(s, None, q12, sc12, wd, sd, ffn, resid, outs["down"], comb)
+                    continue
                 mod.norm_quantize(s, None, xs[4096], gains[1], normed, q4, sc4, mx)
                 if fused_mlp:
                     mod.linear_swiglu_quantize(s, None, q4, sc4, 4096, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx,
@@ -641,14 +651,15 @@ def main() -> int:
             "launches": 8 * synth.LAYERS + 3,
             "chain": "norm_quantize, qkv, quantize, o+residual, norm_quantize, linear_swiglu_quantize, down+residual; lm_head"}
         log(f"decode chain, fused MLP tail: {ms * 1e3:.1f} us ({extras['decode_chain_fused_mlp']['GB/s']} GB/s)")
-        # and with the qkv and o producers folded into their GEMVs
-        # (w8a8_norm_quantize_linear, w8a8_quantize_linear)
+        # and with every producer of a K = 4096 projection folded into its
+        # GEMV (w8a8_norm_quantize_linear, w8a8_quantize_linear,
+        # w8a8_norm_quantize_linear_swiglu)
         ms = time_graph(capture(lambda: layer_chain(fused_mlp=True, fused_producers=True)), 20)
         extras["decode_chain_fused_producers"] = {
             "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-            "launches": 6 * synth.LAYERS + 3,
-            "chain": "norm_quantize_linear (qkv), quantize_linear (o+residual), norm_quantize, "
-                     "linear_swiglu_quantize, down+residual; lm_head"}
+            "launches": 5 * synth.LAYERS + 3,
+            "chain": "norm_quantize_linear (qkv), quantize_linear (o+residual), norm_quantize_linear_swiglu "
+                     "(GEMV + row tail), down+residual; lm_head"}
         log(f"decode chain, fused producers: {ms * 1e3:.1f} us "
             f"({extras['decode_chain_fused_producers']['GB/s']} GB/s)")
         # latency-bound producers at M = 1: per call in a graph of 100

@@ -293,6 +293,30 @@ int w8a8_norm_quantize_linear(void *stream, const float *x,
                               const float *residual, void *out,
                               void *combined, int out_dtype);
 
+/* norm_quantize of one 4096-wide f32 row followed by the decode SwiGLU
+ * projection of its codes (K = 4096), the reference's src/gpu.rs:713 then
+ * :730 with w8a8_linear_swiglu_quantize's outputs, in two launches (the
+ * GEMV with the norm folded in, then the row tail that folds the act
+ * maximum).  No counterpart in the reference.  Bit-identical to
+ * w8a8_norm_quantize then w8a8_linear_swiglu (q_out == NULL) or
+ * w8a8_linear_swiglu_quantize:
+ *   q[4096] (16-byte aligned) and scale[1] of the normalised row, which is
+ *   written to out_norm[4096] when it is not NULL;
+ *   gate[n], up[n], act[n] (F32 or BF16) for w_gate / w_up [n, 4096];
+ *   maxima[0] (required): reset by the norm, then the act maximum folded in;
+ *   q_out[n] and scales_out[1] (both or neither): act quantized with it.
+ * n >= 1.  x and gain must not overlap any output. */
+int w8a8_norm_quantize_linear_swiglu(void *stream, const float *x,
+                                     const float *gain, float *out_norm,
+                                     int8_t *q, float *scale,
+                                     const int8_t *w_gate,
+                                     const float *ws_gate,
+                                     const int8_t *w_up, const float *ws_up,
+                                     size_t n, void *gate, void *up,
+                                     void *act, uint32_t *maxima,
+                                     int8_t *q_out, float *scales_out,
+                                     int out_dtype);
+
 /* quantize of one f32 row of width 4096 (as w8a8_quantize with rows = 1)
  * followed by linear or linear_residual of its codes at M = 1, in one
  * launch: the reference's host linear_residual at decode (src/gpu.rs:364-415:

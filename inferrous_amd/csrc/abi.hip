@@ -713,6 +713,53 @@ int w8a8_norm_quantize_linear(void* stream, const float* x, const float* gain, f
                         out_dtype);
 }
 
+int w8a8_norm_quantize_linear_swiglu(void* stream, const float* x, const float* gain, float* out_norm, int8_t* q,
+                                     float* scale, const int8_t* w_gate, const float* ws_gate, const int8_t* w_up,
+                                     const float* ws_up, size_t n, void* gate, void* up, void* act,
+                                     uint32_t* maxima, int8_t* q_out, float* scales_out, int out_dtype) {
+  if (out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  if (n == 0 || n > kU32Max) return W8A8_ESHAPE;
+  if (!x || !gain || !q || !scale || !w_gate || !ws_gate || !w_up || !ws_up || !gate || !up || !act || !maxima)
+    return W8A8_ENULL;
+  if ((q_out == nullptr) != (scales_out == nullptr)) return W8A8_ENULL;
+  const int oa = out_align(out_dtype);
+  if (!al(x, 4) || !al(gain, 4) || !al(out_norm, 4) || !al(q, 16) || !al(scale, 4) || !al(w_gate, 16) ||
+      !al(ws_gate, 4) || !al(w_up, 16) || !al(ws_up, 4) || !al(gate, oa) || !al(up, oa) || !al(act, oa) ||
+      !al(maxima, 4) || !al(scales_out, 4))
+    return W8A8_EALIGN;
+  const size_t ob = n * (size_t)oa;
+  const struct {
+    const void* p;
+    size_t bytes;
+  } outs[] = {{out_norm, 4096 * 4}, {q, 4096}, {scale, 4}, {gate, ob},  {up, ob},
+              {act, ob},            {maxima, 4}, {q_out, n}, {scales_out, 4}};
+  for (const auto& o : outs)
+    if (overlaps(x, 4096 * 4, o.p, o.bytes) || overlaps(gain, 4096 * 4, o.p, o.bytes)) return W8A8_EARG;
+  if (!ready()) return W8A8_EINIT;
+  ProduceArgs p{};
+  p.x = x;
+  p.gain = gain;
+  p.normed = out_norm;
+  p.q = q;
+  p.scale = scale;
+  p.maxima = maxima;
+  SwigluArgs a{};
+  a.k = 4096;
+  a.n = (uint32_t)n;
+  a.wg = w_gate;
+  a.wsg = ws_gate;
+  a.wu = w_up;
+  a.wsu = ws_up;
+  a.gate = gate;
+  a.up = up;
+  a.act = act;
+  a.out_dtype = out_dtype;
+  a.maxima = maxima;
+  a.q_out = q_out;
+  a.scales_out = scales_out;
+  return hip_status(launch_gemv_swiglu_norm((hipStream_t)stream, p, a));
+}
+
 int w8a8_quantize_linear(void* stream, const float* x, uint32_t width, int8_t* q, float* scale,
                          uint32_t* maxima_reset, const int8_t* w, const float* ws, size_t n,
                          const float* residual, void* out, void* combined, int out_dtype) {

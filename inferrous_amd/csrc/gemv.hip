@@ -343,20 +343,72 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_m1_timed(const int8_t* w
 // asked for, the maxima reset).  One launch instead of two: measured on
 // MI355X in graphs of 36 distinct-weight pairs, norm_quantize + qkv
 // (6144 x 4096) 8.45 -> 7.43 us, quantize + o (4096 x 4096) 6.64 -> 5.30 us.
-// The SwiGLU GEMV's 3,072 workgroups do not hide the repeated norm
-// (19.75 -> 20.2-20.7 us), so it keeps the separate producer.
+// The SwiGLU GEMV takes the same fold with two coordinates per wave
+// (gemv_swiglu_norm, below).
 enum { PROD_QUANT = 1, PROD_NORM = 2 };
+
+struct ProducerLds {
+  float part[256];
+  float inv;
+  uint32_t red[4];
+  alignas(16) int8_t qs[4096];
+};
+
+// The producer's half of a folded kernel, over the workgroup's 256 threads,
+// thread t holding v[i] = x[t + 256 i] (and g[i] = gain[t + 256 i]): the
+// row's codes into L.qs (visible after the next barrier) and its scale,
+// returned.  v is left holding the normalised values (PROD_NORM).
+template <int PROD>
+__device__ __forceinline__ float producer_codes(float (&v)[16], const float (&g)[16], ProducerLds& L) {
+  static_assert(kGemvThreads == 256, "the producers' element order is laid out over 256 threads");
+  const int t = threadIdx.x;
+  uint32_t mb = kFloorBits;
+  if (PROD == PROD_NORM) {
+    const float inv = norm_inv_4096(v, L.part, &L.inv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      v[i] = bf16_rne((v[i] * inv) * g[i]);
+      mb = max(mb, abs_bits_no_nan(v[i]));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mb = max(mb, abs_bits_no_nan(v[i]));
+  }
+  mb = block_max_256(mb, L.red);
+  const float sc = __uint_as_float(mb) / 127.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) L.qs[t + 256 * i] = round_i8(v[i] / sc);
+  return sc;
+}
+
+// Workgroup 0 writes what the producer kernel would have written: the
+// normalised row (when asked for), the scale and the maxima reset now, the
+// codes after the barrier that publishes L.qs (producer_codes_out).
+template <int PROD>
+__device__ __forceinline__ void producer_outputs(const float (&v)[16], float sc, float* normed, float* scale_out,
+                                                 uint32_t* maxima) {
+  if (blockIdx.x != 0) return;
+  const int t = threadIdx.x;
+  if (PROD == PROD_NORM && normed)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) normed[t + 256 * i] = v[i];
+  if (t == 0) {
+    scale_out[0] = sc;
+    if (maxima) maxima[0] = kFloorBits;
+  }
+}
+
+__device__ __forceinline__ void producer_codes_out(const ProducerLds& L, int8_t* q_out) {
+  if (blockIdx.x == 0)
+    *reinterpret_cast<v4i*>(q_out + threadIdx.x * 16) = *reinterpret_cast<const v4i*>(L.qs + threadIdx.x * 16);
+}
 
 template <int R, int EPI, int PROD>
 __global__ __launch_bounds__(kGemvThreads) void gemv_m1_produce(
     const float* x, const float* gain, const int8_t* w, const float* ws, uint32_t n, int dtype,
     const float* residual, void* out, void* combined, int8_t* q_out, float* scale_out, uint32_t* maxima,
     float* normed) {
-  static_assert(kGemvThreads == 256, "the producers' element order is laid out over 256 threads");
-  __shared__ float part[256];
-  __shared__ float inv_shared;
-  __shared__ uint32_t red[4];
-  __shared__ __attribute__((aligned(16))) int8_t qs[4096];
+  __shared__ ProducerLds L;
   const int t = threadIdx.x, lane = t & 63;
   const uint32_t row0 = (blockIdx.x * kGemvWaves + wave_id()) * R;
   // The producer's operands are loaded first: loads complete in issue order,
@@ -365,7 +417,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_m1_produce(
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     v[i] = x[t + 256 * i];
-    if (PROD == PROD_NORM) g[i] = gain[t + 256 * i];
+    g[i] = PROD == PROD_NORM ? gain[t + 256 * i] : 0.f;
   }
   // The epilogue's operands and the weight stream; tail rows recompute the
   // last row (n >= 1).
@@ -379,36 +431,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_m1_produce(
 #pragma unroll
     for (int c = 0; c < 4; ++c) wv[r][c] = load_nt16(p + c * 1024);
   }
-  uint32_t mb = kFloorBits;
-  if (PROD == PROD_NORM) {
-    const float inv = norm_inv_4096(v, part, &inv_shared);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      v[i] = bf16_rne((v[i] * inv) * g[i]);
-      mb = max(mb, abs_bits_no_nan(v[i]));
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) mb = max(mb, abs_bits_no_nan(v[i]));
-  }
-  mb = block_max_256(mb, red);
-  const float sc = __uint_as_float(mb) / 127.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) qs[t + 256 * i] = round_i8(v[i] / sc);
-  if (blockIdx.x == 0) {
-    if (PROD == PROD_NORM && normed)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) normed[t + 256 * i] = v[i];
-    if (t == 0) {
-      scale_out[0] = sc;
-      if (maxima) maxima[0] = kFloorBits;
-    }
-  }
+  const float sc = producer_codes<PROD>(v, g, L);
+  producer_outputs<PROD>(v, sc, normed, scale_out, maxima);
   __syncthreads();
   v4i xq[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) xq[c] = *reinterpret_cast<const v4i*>(qs + c * 1024 + lane * 16);
-  if (blockIdx.x == 0) *reinterpret_cast<v4i*>(q_out + t * 16) = *reinterpret_cast<const v4i*>(qs + t * 16);
+  for (int c = 0; c < 4; ++c) xq[c] = *reinterpret_cast<const v4i*>(L.qs + c * 1024 + lane * 16);
+  producer_codes_out(L, q_out);
   int acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -572,6 +601,73 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_swiglu(SwigluArgs a) {
     store_out(a.gate, c, dtype, tg, g);
     store_out(a.up, c, dtype, tu, u);
     store_out(a.act, c, dtype, 0, v);
+  }
+}
+
+// norm_quantize folded into the M = 1 SwiGLU GEMV (K = 4096), as
+// gemv_m1_produce folds it into linear: every workgroup recomputes the row's
+// codes.  Each wave owns RC consecutive coordinates (their gate and up rows):
+// with one coordinate per wave the 3,072 workgroups' repeated norm did not
+// hide behind the weight stream (norm_quantize + SwiGLU GEMV 19.8 us as two
+// launches, 20.0-20.3 as one); with two, 18.7 us.  The plain GEMV keeps one
+// coordinate per wave (16.5 against 17.3 us with two).
+template <int RC>
+__global__ __launch_bounds__(kGemvThreads) void gemv_swiglu_norm(
+    const float* x, const float* gain, const int8_t* wg, const float* wsg, const int8_t* wu, const float* wsu,
+    uint32_t n, int dtype, void* gate, void* up, void* act, int8_t* q_out, float* scale_out, uint32_t* maxima,
+    float* normed) {
+  __shared__ ProducerLds L;
+  const int t = threadIdx.x, lane = t & 63;
+  const uint32_t c0 = (blockIdx.x * kGemvWaves + wave_id()) * RC;
+  float v[16], g[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    v[i] = x[t + 256 * i];
+    g[i] = gain[t + 256 * i];
+  }
+  // epilogue operands and weights; tail coordinates recompute the last (n >= 1)
+  float sg[RC], su[RC];
+  v4i wgv[RC][4], wuv[RC][4];
+#pragma unroll
+  for (int rc = 0; rc < RC; ++rc) {
+    const uint32_t cr = min(c0 + rc, n - 1);
+    sg[rc] = wsg[cr];
+    su[rc] = wsu[cr];
+    const int8_t* pg = wg + (size_t)cr * 4096 + lane * 16;
+    const int8_t* pu = wu + (size_t)cr * 4096 + lane * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wgv[rc][i] = load_nt16(pg + i * 1024);
+      wuv[rc][i] = load_nt16(pu + i * 1024);
+    }
+  }
+  const float sc = producer_codes<PROD_NORM>(v, g, L);
+  producer_outputs<PROD_NORM>(v, sc, normed, scale_out, maxima);
+  __syncthreads();
+  v4i xq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xq[i] = *reinterpret_cast<const v4i*>(L.qs + i * 1024 + lane * 16);
+  producer_codes_out(L, q_out);
+#pragma unroll
+  for (int rc = 0; rc < RC; ++rc) {
+    int ag = 0, au = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ag = dot16(xq[i], wgv[rc][i], ag);
+      au = dot16(xq[i], wuv[rc][i], au);
+    }
+    const int tg = wave_sum_uniform(ag);
+    const int tu = wave_sum_uniform(au);
+    const float gv = dequant(tg, sc, sg[rc]);
+    const float uv = dequant(tu, sc, su[rc]);
+    const float av = silu_mul(gv, uv);
+    asm volatile("" ::"v"(av), "s"(dtype));
+    const uint32_t c = c0 + rc;
+    if (c < n && lane == 0) {
+      store_out(gate, c, dtype, tg, gv);
+      store_out(up, c, dtype, tu, uv);
+      store_out(act, c, dtype, 0, av);
+    }
   }
 }
 
@@ -857,6 +953,20 @@ hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {
     return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !a.maxima) return e;
+  hipLaunchKernelGGL(swiglu_row_tail<true>, dim3(1), dim3(kRowTailThreads), 0, st, a.act, a.n, a.out_dtype,
+                     a.maxima, a.q_out, a.scales_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a) {
+  if (a.n == 0 || a.k != 4096 || !a.maxima) return hipErrorInvalidValue;
+  constexpr int RC = 2;
+  const dim3 grid((a.n + RC * kGemvWaves - 1) / (RC * kGemvWaves));
+  hipLaunchKernelGGL(gemv_swiglu_norm<RC>, grid, dim3(kGemvThreads), 0, st, p.x, p.gain, a.wg, a.wsg, a.wu, a.wsu,
+                     a.n, a.out_dtype, a.gate, a.up, a.act, p.q, p.scale, p.maxima, p.normed);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // the norm reset maxima[0] inside the GEMV; the row tail folds into it
   hipLaunchKernelGGL(swiglu_row_tail<true>, dim3(1), dim3(kRowTailThreads), 0, st, a.act, a.n, a.out_dtype,
                      a.maxima, a.q_out, a.scales_out);
   return hipGetLastError();

@@ -106,6 +106,10 @@ struct ProduceArgs {
   int out_dtype;
 };
 hipError_t launch_gemv_produce(hipStream_t st, const ProduceArgs& p);
+// norm_quantize (p: x, gain, normed, q, scale; p.maxima == a.maxima) folded
+// into the M = 1 SwiGLU GEMV (a: k = 4096, maxima required), then the row
+// tail that folds the act maximum (and quantizes act when a.q_out is set).
+hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a);
 // Diagnostics: the one-matrix M = 1 GEMV with per-wave clock stamps.
 size_t gemv_timeline_waves(size_t n, uint32_t k);
 hipError_t launch_gemv_timeline(hipStream_t st, const int8_t* q, const float* asc, const int8_t* w,

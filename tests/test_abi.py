@@ -132,9 +132,10 @@ def test_diag_timeline_validation_precedes_device():
 
 @pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
 def test_producer_linear_validation_precedes_device():
-    """w8a8_norm_quantize_linear / w8a8_quantize_linear reject malformed
-    calls on the host, including any output that shares bytes with the row
-    every workgroup reads."""
+    """w8a8_norm_quantize_linear, w8a8_quantize_linear and
+    w8a8_norm_quantize_linear_swiglu reject malformed calls on the host,
+    including any output that shares bytes with the row every workgroup
+    reads."""
     L = _lib.lib()
     B = A + 0x100000  # outputs, clear of x [A, A + 16 KiB) and gain [A + 16 KiB, A + 32 KiB)
 
@@ -166,6 +167,26 @@ def test_producer_linear_validation_precedes_device():
     assert nql(norm=A + 0x10) == _lib.EARG             # the normalised row over x
     assert nql(out=A + 0x4100) == _lib.EARG            # out over the gains
     assert nql(q=A + 0x3ff0) == _lib.EARG              # codes over x's last bytes
+
+    def nqs(**kw):
+        a = dict(x=A, gain=A + 0x4000, norm=None, q=B + 0x8000, sc=B + 0x9000, wg=B + 0x10000, sg=B + 0x20000,
+                 wu=B + 0x30000, su=B + 0x40000, n=12288, gate=B + 0x50000, up=B + 0x60000, act=B + 0x70000,
+                 mx=B + 0x9010, qo=B + 0x80000, so=B + 0x9020, dt=_lib.OUT_F32)
+        a.update(kw)
+        return L.w8a8_norm_quantize_linear_swiglu(None, a["x"], a["gain"], a["norm"], a["q"], a["sc"], a["wg"],
+                                                  a["sg"], a["wu"], a["su"], a["n"], a["gate"], a["up"], a["act"],
+                                                  a["mx"], a["qo"], a["so"], a["dt"])
+
+    assert nqs() == _lib.EINIT
+    assert nqs(qo=None, so=None) == _lib.EINIT
+    assert nqs(n=0) == _lib.ESHAPE
+    assert nqs(dt=_lib.OUT_I32) == _lib.EARG
+    assert nqs(mx=None) == _lib.ENULL                  # the norm resets it, the row tail folds into it
+    assert nqs(so=None) == _lib.ENULL                  # q_out and scales_out go together
+    assert nqs(act=None) == _lib.ENULL and nqs(gain=None) == _lib.ENULL
+    assert nqs(wu=B + 0x30008) == _lib.EALIGN and nqs(q=B + 0x8008) == _lib.EALIGN
+    assert nqs(act=A + 0x100) == _lib.EARG             # act over x
+    assert nqs(mx=A + 0x4000) == _lib.EARG             # maxima over the gains
     assert ql() == _lib.EINIT
     assert ql(res=None, comb=None) == _lib.EINIT
     assert ql(width=4095) == _lib.ESHAPE and ql(width=12288) == _lib.ESHAPE

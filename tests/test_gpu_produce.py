@@ -1,7 +1,9 @@
 """GPU parity of the producers folded into the decode GEMV's prologue:
 `w8a8_norm_quantize_linear` (norm_quantize, src/kernels.rs:476-575, then
 linear / linear_residual) and `w8a8_quantize_linear` (quantize,
-src/kernels.rs:433-451, then the same), one launch each.
+src/kernels.rs:433-451, then the same), one launch each, and
+`w8a8_norm_quantize_linear_swiglu` (norm_quantize, then linear_swiglu,
+src/kernels.rs:619-695, and optionally the act's quantize_with_max).
 
 Every workgroup recomputes the row's codes with the producer's arithmetic, so
 every output must equal the two-call sequence bit for bit: the codes, the
@@ -230,3 +232,70 @@ def test_producer_linear_graph_replay(env):
         got = [b.to_host_vec(s) for b in (o1, o2, c2, q, sc)]
         for a, b in zip(got, want):
             assert same_bits(a, b)
+
+
+def run_swiglu_both(env, x, gain, wg, sg, wu, su, dtype, quantize):
+    """(separate calls, folded call): norm_quantize then linear_swiglu or
+    linear_swiglu_quantize, against norm_quantize_linear_swiglu."""
+    _, mod, s = env
+    n = sg.size
+    xb, gb = dev(s, x), dev(s, gain)
+    wgb, sgb, wub, sub = dev(s, wg), dev(s, sg), dev(s, wu), dev(s, su)
+    res = {}
+    for mode in ("calls", "folded"):
+        q = DeviceBuffer.zeroed(s, 4096, np.int8)
+        sc = DeviceBuffer.zeroed(s, 1, np.float32)
+        nb = DeviceBuffer.zeroed(s, 4096, np.float32)
+        mx = dev(s, np.array([JUNK], np.uint32))
+        gate, up, act = (DeviceBuffer.zeroed(s, n, dtype) for _ in range(3))
+        qo = DeviceBuffer.zeroed(s, n, np.int8) if quantize else None
+        so = DeviceBuffer.zeroed(s, 1, np.float32) if quantize else None
+        if mode == "calls":
+            mod.norm_quantize(s, None, xb, gb, nb, q, sc, mx)
+            if quantize:
+                mod.linear_swiglu_quantize(s, None, q, sc, 4096, wgb, sgb, gate, wub, sub, up, act, mx, qo, so)
+            else:
+                mod.linear_swiglu(s, None, q, sc, 4096, wgb, sgb, gate, wub, sub, up, act, mx)
+        else:
+            mod.norm_quantize_linear_swiglu(s, None, xb, gb, nb, q, sc, wgb, sgb, gate, wub, sub, up, act, mx,
+                                            qo, so)
+        s.synchronize()
+        res[mode] = dict(q=q.to_host_vec(s), sc=sc.to_host_vec(s), normed=nb.to_host_vec(s),
+                         mx=mx.to_host_vec(s), gate=gate.to_host_vec(s), up=up.to_host_vec(s),
+                         act=act.to_host_vec(s), qo=qo.to_host_vec(s) if quantize else None,
+                         so=so.to_host_vec(s) if quantize else None)
+    return res["calls"], res["folded"]
+
+
+def nan_same(a, b):
+    if a.dtype == np.float32:
+        return bool(((bits(a) == bits(b)) | (np.isnan(a) & np.isnan(b))).all())
+    return np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("quantize", [False, True])
+@pytest.mark.parametrize("dtype", [np.float32, np.uint16])
+@pytest.mark.parametrize("n,kind", [(12288, "normal"), (1, "normal"), (33, "normal"), (8191, "normal"),
+                                    (12288, "zero"), (12288, "nan")])
+def test_norm_swiglu_matches_calls(env, quantize, dtype, n, kind):
+    """Two coordinates per wave: n = 1 and 33 leave a ragged last wave (its
+    tail coordinate clamped); n = 8191 an odd count.  gate, up and act,
+    the codes, scale, normalised row, the maximum (reset, then folded) and
+    the act's codes and scale all equal the separate calls' bits."""
+    print(f"norm+swiglu n={n} {kind} {np.dtype(dtype).name} quantize={quantize}", flush=True)
+    rng = np.random.default_rng(n + (7 if quantize else 0) + len(kind))
+    x = make_row(rng, kind)
+    gain = (1 + 0.3 * rng.standard_normal(4096)).astype(F32)
+    wg = rng.integers(-127, 128, (n, 4096), dtype=np.int8)
+    wu = rng.integers(-127, 128, (n, 4096), dtype=np.int8)
+    sg = (rng.random(n) / 64 + 1e-4).astype(F32)
+    su = (rng.random(n) / 64 + 1e-4).astype(F32)
+    calls, folded = run_swiglu_both(env, x, gain, wg, sg, wu, su, dtype, quantize)
+    for key in ("q", "sc", "normed", "mx", "gate", "up", "act") + (("qo", "so") if quantize else ()):
+        assert nan_same(folded[key], calls[key]), key
+    if kind == "normal":
+        _, wq, wsc, _ = oracle.norm_quantize(x[None, :], gain)
+        assert np.array_equal(folded["q"], wq.reshape(-1)) and np.array_equal(bits(folded["sc"]), bits(wsc))
+        acc, of, ob = oracle.linear(wq.reshape(1, -1), wsc, wg, sg, 4096, threads=8)
+        want_gate = ob if dtype == np.uint16 else of
+        assert same_bits(folded["gate"], want_gate), "gate against the oracle"
