@@ -64,19 +64,32 @@ int check_linear(const int8_t* q, const float* asc, size_t m, const int8_t* w, c
   return W8A8_OK;
 }
 
-// dot4 GEMV for m <= 4, MFMA beyond: the measured crossover on MI355X
-// (gate_up / down at m = 1..64) lies between m = 4 and m = 8.  At m = 4 the
-// dot4 GEMV (chunk order rotated per row group) streams gate_up at 4.8 TB/s
-// and down at 3.5 against the MFMA family's 4.4 and 3.0; at m = 8 the MFMA
-// family leads, 4.86 / 3.37 against 3.62 / 2.79.
+// AUTO route of one projection: the dot4 GEMV for m <= 2, the MFMA family
+// from m = 3.  Measured on MI355X through this ABI (graphs of 16
+// distinct-weight launches, random operands), dot4 against MFMA at
+// m = 2 / 3 / 4: qkv 7.7 / 8.9 / 9.3 against 8.4 / 8.6 / 8.8 us, o 5.85 /
+// 7.3 / 7.45 against 7.1 / 7.1 / 7.2, gate_up 17.7 / 19.7 / 20.6 against
+// 18.0 / 18.0 / 18.0, down 11.7 / 14.0 / 14.4 against 13.2 / 13.3 / 13.4.
+// Down's MFMA figure is its split-K plan, which needs the caller's
+// workspace; without it (16.8 us) m = 3 and 4 keep the dot4 GEMV.  The
+// grouped projections keep one dot4 launch for every matrix up to m = 4
+// (kDot4MaxM).
 constexpr size_t kDot4MaxM = 4;
+constexpr size_t kDot4AutoMaxM = 2;
+
+static int auto_path(size_t m, size_t n, uint32_t k, size_t workspace_bytes) {
+  if (m <= kDot4AutoMaxM) return W8A8_PATH_DOT4;
+  if (m > kDot4MaxM) return W8A8_PATH_MFMA;
+  const size_t need = gemm_workspace_bytes((uint32_t)m, (uint32_t)n, k);
+  return need == 0 || workspace_bytes >= need ? W8A8_PATH_MFMA : W8A8_PATH_DOT4;
+}
 
 int run_linear(hipStream_t st, const int8_t* q, const float* asc, size_t m, const int8_t* w,
                const float* ws, size_t n, uint32_t k, void* out, int out_dtype, int path,
                const float* residual, void* combined, void* workspace = nullptr,
                size_t workspace_bytes = 0) {
   if (m == 0 || n == 0) return W8A8_OK;
-  if (path == W8A8_PATH_AUTO) path = m <= kDot4MaxM ? W8A8_PATH_DOT4 : W8A8_PATH_MFMA;
+  if (path == W8A8_PATH_AUTO) path = auto_path(m, n, k, workspace ? workspace_bytes : 0);
   if (path == W8A8_PATH_DOT4) {
     GemvArgs a{};
     a.q = q;
@@ -501,7 +514,7 @@ int w8a8_linear_residual(void* stream, const int8_t* q, const float* asc, size_t
 }
 
 size_t w8a8_linear_workspace_bytes(size_t m, size_t n, uint32_t k) {
-  if (m <= kDot4MaxM || m > kU32Max || n > kU32Max) return 0;
+  if (m == 0 || m > kU32Max || n > kU32Max) return 0;
   return gemm_workspace_bytes((uint32_t)m, (uint32_t)n, k);
 }
 

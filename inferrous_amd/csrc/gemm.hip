@@ -31,11 +31,12 @@
 //    Workgroups are numbered XCD-aware (below).  Tile shape per problem is
 //    chosen by the host from the tile count.  With a caller workspace, some
 //    shapes run split-K (i32 slabs + splitk_epilogue).
-//  * gemm_tall (8 <= M <= 256, k % 128 == 0, where its plan applies; M tiles
-//    of 64, 160 or 256 rows): one M tile holds every
-//    activation row, so each weight tile streams from HBM once; the eight
-//    waves are stacked along M and those past M only move data; activation
-//    rows past M are never loaded; split-K on narrow n.
+//  * gemm_tall (M <= 256, k % 128 == 0, where its plan applies; M tiles of
+//    64, 160 or 256 rows): one M tile holds every activation row, so each
+//    weight tile streams from HBM once; the waves hold 32 x 32 output blocks
+//    one each (M <= 64) or 32-row slices of all BN columns, and those
+//    holding none only move data; activation rows past M are never loaded;
+//    split-K on narrow n.
 //  * gemm_skinny (small M on narrow n, HBM-bound, 16x16x64 MFMA): one
 //    workgroup owns 16 weight rows; its S waves split K and stream their
 //    weight fragments straight from HBM into MFMA B operands (no LDS round
@@ -584,8 +585,20 @@ __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
 // Prefill / small-batch GEMM for M <= MA (gemm_tall, MA = 64, 160 or 256).  One M tile
 // of MA rows holds every activation row, so each weight tile is read from
 // HBM once, and no DMA or MFMA goes to a second M tile holding a few rows.
-// The eight waves are stacked along M (wave w: rows 32w .. 32w + 31, all BN
-// columns); a wave whose rows all lie past M only moves data.
+// MA = 160 and 256: the eight waves are stacked along M (wave w: rows
+// 32w .. 32w + 31, all BN columns), so a wave reads one activation fragment
+// per k step for its BN / 32 MFMAs.  MA = 64 (M <= 64, one or two 32-row
+// blocks): the 32 x 32 output blocks are dealt to the waves one each (block
+// b = row block * BN / 32 + column block goes to wave b), so the SIMDs (wave
+// w runs on SIMD w % 4) share the MFMAs instead of one or two waves holding
+// them all.  Measured on MI355X, graphs of 16 distinct-weight launches with
+// random operands, rows-per-wave -> one block per wave: at M = 16 qkv 11.7
+// -> 10.6 us, o 9.3 -> 8.6, gate_up 21.0-21.4 -> 18.1, down 15.6 -> 13.8;
+// at M = 64 qkv 13.0 -> 12.0, o 10.9 -> 10.4, gate_up 22.1-23.3 -> 20.0-20.4,
+// down 17.6-18.2 -> 16.3.  With more row blocks the same dealing reads twice
+// the LDS fragment bytes per MFMA for no better balance (M = 129: level;
+// M = 200: gate_up 33.0 -> 37.8), so those tiles keep rows per wave.
+// A wave that holds no block only moves data.
 //
 // Rings as in gemm_dma: activations (SA slots of MA rows; the lines are
 // shared by every workgroup and come from L2 or MALL) and weights (SB slots;
@@ -687,18 +700,42 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
   int off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) off[i] = fr * 128 + (((2 * i + fh) ^ ((fr >> 1) & 7)) * 16);
-  v16i acc[FN];
-#pragma unroll
-  for (int j = 0; j < FN; ++j) acc[j] = v16i{};
-  auto rd = [&](uint32_t kt, int i, v4i& af, v4i (&bf)[FN]) {
-    af = *(const v4i*)(ldsA + (kt % SA) * ASL + (32 * wave) * 128 + off[i]);
-    const int8_t* bb = ldsB + (kt % SB) * BSL;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(bb + (32 * j) * 128 + off[i]);
+  // Stage pipeline shared by both mappings: fragments of sub-step i + 1 are
+  // read while the MFMAs of sub-step i issue.  rd(kt, i, f) reads sub-step i
+  // of stage kt into f; mm(f) issues its MFMAs.
+  auto pipeline = [&](auto& f0, auto& f1, auto rd, auto mm) {
+    batch(0);
+    rd(0, 0, f0);
+    for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+      rd(kt, 1, f1);
+      mm(f0);
+      rd(kt, 2, f0);
+      mm(f1);
+      rd(kt, 3, f1);
+      mm(f0);
+      wait_next(kt);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of stage kt returned
+      __builtin_amdgcn_s_barrier();
+      batch(kt + 1);
+      rd(kt + 1, 0, f0);
+      mm(f1);
+    }
+    rd(KT - 1, 1, f1);
+    mm(f0);
+    rd(KT - 1, 2, f0);
+    mm(f1);
+    rd(KT - 1, 3, f1);
+    mm(f0);
+    mm(f1);
   };
-  auto mm = [&](const v4i& af, const v4i (&bf)[FN]) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[j] = mfma32(af, bf[j], acc[j]);
+  // rows past M, or no block: this wave only moves its share of the data
+  auto move_only = [&]() {
+    batch(0);
+    for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+      wait_next(kt);
+      __builtin_amdgcn_s_barrier();
+      batch(kt + 1);
+    }
   };
 
   // Prologue: stages 0 .. SB - 2 (activations up to SA - 2), stage by stage;
@@ -711,40 +748,51 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
   if (KT >= (uint32_t)SB - 1) wait_vmcnt_dyn((SA - 2) * na + (SB - 2) * nb);
   else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
-  if (32u * wave < a.m) {
-    v4i a0, b0[FN], a1, b1[FN];
-    batch(0);
-    rd(0, 0, a0, b0);
-    for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
-      rd(kt, 1, a1, b1);
-      mm(a0, b0);
-      rd(kt, 2, a0, b0);
-      mm(a1, b1);
-      rd(kt, 3, a1, b1);
-      mm(a0, b0);
-      wait_next(kt);
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of stage kt returned
-      __builtin_amdgcn_s_barrier();
-      batch(kt + 1);
-      rd(kt + 1, 0, a0, b0);
-      mm(a1, b1);
+
+  if constexpr (MA == 64) {
+    // one 32 x 32 block per wave: block `wave` of the (M / 32) x FN grid
+    const uint32_t T = (a.m + 31) / 32 * FN;
+    static_assert(2 * FN <= 8, "one block per wave");
+    if ((uint32_t)wave < T) {
+      const uint32_t mb = (uint32_t)wave / FN, nbk = (uint32_t)wave % FN;
+      const int8_t* const aa = ldsA + mb * 32 * 128;
+      const int8_t* const bb = ldsB + nbk * 32 * 128;
+      struct Frag { v4i a, b; };
+      v16i acc = v16i{};
+      Frag f0, f1;
+      pipeline(f0, f1,
+               [&](uint32_t kt, int i, Frag& f) {
+                 f.a = *(const v4i*)(aa + (kt % SA) * ASL + off[i]);
+                 f.b = *(const v4i*)(bb + (kt % SB) * BSL + off[i]);
+               },
+               [&](const Frag& f) { acc = mfma32(f.a, f.b, acc); });
+      const v16i blocks[1][1] = {{acc}};
+      store_blocks<EP, 1, 1>(a, blocks, 32 * mb, n0 + 32 * nbk, lane);
+    } else {
+      move_only();
     }
-    rd(KT - 1, 1, a1, b1);
-    mm(a0, b0);
-    rd(KT - 1, 2, a0, b0);
-    mm(a1, b1);
-    rd(KT - 1, 3, a1, b1);
-    mm(a0, b0);
-    mm(a1, b1);
-    const v16i (&blocks)[1][FN] = *reinterpret_cast<const v16i(*)[1][FN]>(&acc);
-    store_blocks<EP, 1, FN>(a, blocks, 32 * wave, n0, lane);
   } else {
-    // rows past M: this wave only moves its share of the data
-    batch(0);
-    for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
-      wait_next(kt);
-      __builtin_amdgcn_s_barrier();
-      batch(kt + 1);
+    if (32u * wave < a.m) {
+      struct Frag { v4i a, b[FN]; };
+      v16i acc[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[j] = v16i{};
+      Frag f0, f1;
+      pipeline(f0, f1,
+               [&](uint32_t kt, int i, Frag& f) {
+                 f.a = *(const v4i*)(ldsA + (kt % SA) * ASL + (32 * wave) * 128 + off[i]);
+                 const int8_t* bb = ldsB + (kt % SB) * BSL;
+#pragma unroll
+                 for (int j = 0; j < FN; ++j) f.b[j] = *(const v4i*)(bb + (32 * j) * 128 + off[i]);
+               },
+               [&](const Frag& f) {
+#pragma unroll
+                 for (int j = 0; j < FN; ++j) acc[j] = mfma32(f.a, f.b[j], acc[j]);
+               });
+      const v16i (&blocks)[1][FN] = *reinterpret_cast<const v16i(*)[1][FN]>(&acc);
+      store_blocks<EP, 1, FN>(a, blocks, 32 * wave, n0, lane);
+    } else {
+      move_only();
     }
   }
 }
@@ -907,7 +955,7 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
   return kt % splits == 0 && kt / splits >= 4;
 }
 
-// gemm_tall plan for 8 <= m <= 256 (measured on MI355X on the Qwen3-8B
+// gemm_tall plan for 1 <= m <= 256 (measured on MI355X on the Qwen3-8B
 // projection shapes at M = 16, 64, 65, 80, 100, 128 and 129): 96-column
 // tiles when they alone give about one tile per CU; otherwise split K four
 // ways (two when K is short), with 96- or 64-column tiles, to reach about one
@@ -917,10 +965,18 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
 // with streamed slabs the split route also beats gemm_dma's split-K 2 on
 // qkv and o (qkv at M = 65 / 100 / 128 12.6 / 14.1 / 14.5 against
 // 13.2-13.3 / 14.6 / 15.5, o 10.9 / 11.6 / 12.7 against 12.0 / 12.7 / 13.2).
+// Below m = 16 the plan applies to the wide shapes and to long K only, where
+// it beats gemm_skinny (graphs of 16 distinct-weight launches, random
+// operands, m = 1..6: gate_up 17.9-18.1 against 21.2-24.0 us, down at
+// K = 12288 13.1-13.5 against 16.7-17.1).  On qkv and o at K = 4096 the
+// skinny kernel's split-K leads up to there: qkv at m = 1..6 / 8 / 12 / 16
+// / 24 8.3-9.1 / 9.5 / 10.6 / 11.5 / 14.1 us against 9.7-10.1 / 10.3 / 10.5
+// / 10.5 / 10.9, o 6.9-7.4 / 7.5 / 7.7 / 7.9 / 9.6 against 8.1-8.4 / 8.3 /
+// 8.5 / 8.7 / 9.0.
 // Returns false when no plan applies (the gemm_dma or gemm_skinny routes
 // then run).  ma: the M tile (64, 160 or 256 rows).
 static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits, int& ma) {
-  if (m < 8 || m > 256 || k % 128 != 0) return false;
+  if (m == 0 || m > 256 || k % 128 != 0) return false;
   ma = m <= 64 ? 64 : m <= 160 ? 160 : 256;
   const uint32_t kt = k / 128, t96 = (n + 95) / 96;
   if (t96 >= 224) {
@@ -929,6 +985,7 @@ static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& spl
     return true;
   }
   if (n % 4 != 0) return false;  // the split-K epilogue works on column quads
+  if (m < 16 && k < 8192) return false;
   splits = (kt % 4 == 0 && kt / 4 >= 4) ? 4 : (kt % 2 == 0 && kt / 2 >= 4) ? 2 : 1;
   if (splits == 1) return false;
   bn = t96 * splits >= 224 ? 96 : 64;
@@ -1044,7 +1101,7 @@ static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   if (a.m == 0 || a.n == 0) return hipSuccess;
   const unsigned nb16 = (a.n + 15) / 16;
-  // 8 <= m <= 256 goes to gemm_tall when its plan applies.
+  // m <= 256 goes to gemm_tall when its plan applies.
   // Otherwise, for small m: from m = 8 the 8-wave kernel with 64-row tiles
   // streams the weights faster when n gives at least 128 tiles; below that
   // the skinny kernel's split-K keeps more CUs busy.

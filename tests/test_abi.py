@@ -309,7 +309,9 @@ def test_fused_and_workspace_entries_validation():
     assert nq(x=None) == _lib.ENULL and nq(maxima=None) == _lib.ENULL
     assert nq(out=A + 2) == _lib.EALIGN
     # linear_ex: the split-K workspace is optional, never required
-    assert L.w8a8_linear_workspace_bytes(1, 4096, 12288) == 0      # dot4 path: none
+    # the MFMA family's split plan for down at m = 1 (4 slabs); AUTO runs dot4 there
+    assert L.w8a8_linear_workspace_bytes(1, 4096, 12288) == 4 * 1 * 4096 * 4
+    assert L.w8a8_linear_workspace_bytes(4, 4096, 4096) == 0       # skinny kernel: none
     assert L.w8a8_linear_workspace_bytes(512, 4096, 12288) > 0     # 128x128 split in two
     assert L.w8a8_linear_workspace_bytes(512, 4096, 12288) == 2 * 512 * 4096 * 4
     ex = lambda **kw: L.w8a8_linear_ex(  # noqa: E731

@@ -584,12 +584,14 @@ def test_errors_raise_not_fall_back(env):
                                    (100, 96, 12288), (255, 1024, 4096), (100, 4096, 12288), (65, 4100, 12288),
                                    (128, 4096, 4096),
                                    (129, 4100, 4096), (64, 4100, 12288), (512, 4100, 12288),
-                                   (16, 4100, 12288), (100, 1024, 4096)])
+                                   (16, 4100, 12288), (100, 1024, 4096), (3, 4100, 12288), (7, 1024, 8192)])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     """w8a8_linear_ex with a workspace (split-K partials + exact i32 epilogue)
     equals the call without one and the oracle, bit for bit -- also on a
     second call with the same workspace, which carries nothing between calls.
+    Below M = 16 only K >= 8192 splits (3 x 4100 x 12288 under AUTO's MFMA
+    route from M = 3, 7 x 1024 x 8192).
     The shapes cover both slab policies with the 16-byte and the 4-column
     epilogue each: streamed (gemm_tall from 3 MiB of slabs, e.g. 129 x 4096 x
     4096 and 64 x 4100 x 12288) and plain (smaller gemm_tall sets such as
@@ -731,15 +733,19 @@ def test_linear_split_k_unaligned_outputs(env):
     assert np.array_equal(comb.to_host_vec(s)[1:], want_comb)
 
 
-@pytest.mark.parametrize("m", [8, 33, 64, 65, 100, 128, 129, 193, 256])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8, 16, 33, 40, 64, 65, 100, 128, 129, 193, 256])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_one_m_tile_wide_n(env, m, dtype, res):
-    """8 <= M <= 256 on a wide N (the gate_up regime): one M tile,
-    waves past M idle, activation rows past M never loaded, a ragged last
-    column tile; bit-exact against the oracle with and without a workspace."""
+    """1 <= M <= 256 on a wide N (the gate_up regime): one M tile, one
+    32 x 32 block per wave up to M = 64 (one to six blocks busy) and 32-row
+    slices above, waves without work idle, activation rows past M never
+    loaded, a ragged last column tile; bit-exact against the oracle with and
+    without a workspace.  M <= 2 forces the MFMA family (AUTO runs dot4
+    there)."""
     from inferrous_amd import _lib
     ctx, mod, s = env
     n, k = 21601, 1024
+    path = _lib.PATH_MFMA if m <= 2 else _lib.PATH_AUTO
     print(f"one-M-tile m={m} n={n} k={k} {np.dtype(dtype).name} res={res}", flush=True)
     lib = _lib.lib()
     rng = np.random.default_rng(m * 7 + 3)
@@ -759,7 +765,7 @@ def test_linear_one_m_tile_wide_n(env, m, dtype, res):
         comb = DeviceBuffer.zeroed(s, m * n, dtype) if res else None
         _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k,
                                       dres.ptr if res else None, out.ptr,
-                                      comb.ptr if res else None, dt, _lib.PATH_AUTO, wp, wb))
+                                      comb.ptr if res else None, dt, path, wp, wb))
         outs.append((out.to_host_vec(s), comb.to_host_vec(s) if res else None))
     assert np.array_equal(outs[1][0].view(np.uint8), outs[0][0].view(np.uint8))
     acc, of, ob = oracle.linear(q, asc, w, ws, k, threads=8)
