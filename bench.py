@@ -221,9 +221,10 @@ def ragged_profile_run() -> int:
 def chain_profile_run() -> int:
     """Workload for a kernel-trace profile of the decode layer chain
     (src/gpu.rs:571-790 order) at M = 1: 8 layers of distinct weights, the
-    reference call sequence, the chain with linear_swiglu_quantize, and that
-    chain with the qkv and o producers folded into their GEMVs, each captured
-    once and replayed 5 times."""
+    reference call sequence, the chain with linear_swiglu_quantize, that
+    chain with every K = 4096 producer folded into its GEMV, and the same with
+    the MLP block as norm_quantize_mlp (the act row tail folded into the down
+    GEMV), each captured once and replayed 5 times."""
     from inferrous_amd import CudaContext, DeviceBuffer, Graph, load, synth
     ctx = CudaContext(0)
     mod = load(ctx)
@@ -256,12 +257,17 @@ def chain_profile_run() -> int:
 
     def chain(mode: int):
         # 0: the reference's calls; 1: linear_swiglu_quantize for the MLP
-        # pair; 2: every K = 4096 producer folded into its GEMV
+        # pair; 2: every K = 4096 producer folded into its GEMV; 3: and the
+        # MLP block in two launches
         for (mats, (wg_, sg_, wu_, su_)) in layers:
             (wqkv, sqkv), (wo, so), _, (wd, sd) = mats
-            if mode == 2:
+            if mode >= 2:
                 mod.norm_quantize_linear(s, None, x, gains[0], normed, q4, sc4, mx, wqkv, sqkv, qkv)
                 mod.quantize_linear(s, None, x, q4, sc4, wo, so, o, resid, comb)
+                if mode == 3:
+                    mod.norm_quantize_mlp(s, None, x, gains[1], normed, q4, sc4, wg_, sg_, gbuf, wu_, su_, ubuf,
+                                          act, mx, wd, sd, down, resid, comb, q12, sc12)
+                    continue
                 mod.norm_quantize_linear_swiglu(s, None, x, gains[1], normed, q4, sc4, wg_, sg_, gbuf, wu_, su_,
                                                 ubuf, act, mx, q12, sc12)
                 mod.linear_residual(s, None, q12, sc12, wd, sd, ffn, resid, down, comb)
@@ -279,7 +285,8 @@ def chain_profile_run() -> int:
                 mod.linear_swiglu(s, None, q4, sc4, h, wg_, sg_, gbuf, wu_, su_, ubuf, act, mx)
                 mod.linear_quantize_with_max(s, None, act, ffn, mx, q12, sc12, wd, sd, down, resid, comb)
 
-    for mode, label in ((0, "reference calls"), (1, "fused MLP tail"), (2, "fused producers")):
+    for mode, label in ((0, "reference calls"), (1, "fused MLP tail"), (2, "fused producers"),
+                        (3, "fused MLP block")):
         chain(mode)
         s.synchronize()
         g = Graph(s)
@@ -615,10 +622,10 @@ def main() -> int:
                     mod.quantize(s, None, xs[4096], 4096, q4, sc4)
                     mod.linear_residual(s, None, q4, sc4, wo, so, 4096, resid, outs["o"], comb)
                 if fused_producers:
-                    # norm_quantize folded into the SwiGLU GEMV (+ its row tail)
-                    mod.norm_quantize_linear_swiglu(s, None, xs[4096], gains[1], normed, q4, sc4, wg_, sg_, gbuf,
-                                                    wu_, su_, ubuf, act, mx, q12, sc12)
-                    mod.linear_residual(s, None, q12, sc12, wd, sd, ffn, resid, outs["down"], comb)
+                    # the MLP block in two launches: norm_quantize folded into
+                    # the SwiGLU GEMV, the act row tail into the down GEMV
+                    mod.norm_quantize_mlp(s, None, xs[4096], gains[1], normed, q4, sc4, wg_, sg_, gbuf, wu_, su_,
+                                          ubuf, act, mx, wd, sd, outs["down"], resid, comb, q12, sc12)
                     continue
                 mod.norm_quantize(s, None, xs[4096], gains[1], normed, q4, sc4, mx)
                 if fused_mlp:
@@ -651,15 +658,16 @@ def main() -> int:
             "launches": 8 * synth.LAYERS + 3,
             "chain": "norm_quantize, qkv, quantize, o+residual, norm_quantize, linear_swiglu_quantize, down+residual; lm_head"}
         log(f"decode chain, fused MLP tail: {ms * 1e3:.1f} us ({extras['decode_chain_fused_mlp']['GB/s']} GB/s)")
-        # and with every producer of a K = 4096 projection folded into its
-        # GEMV (w8a8_norm_quantize_linear, w8a8_quantize_linear,
-        # w8a8_norm_quantize_linear_swiglu)
+        # and with every producer folded into the GEMV that consumes it
+        # (w8a8_norm_quantize_linear, w8a8_quantize_linear, and the MLP block
+        # as w8a8_norm_quantize_mlp)
         ms = time_graph(capture(lambda: layer_chain(fused_mlp=True, fused_producers=True)), 20)
         extras["decode_chain_fused_producers"] = {
             "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-            "launches": 5 * synth.LAYERS + 3,
-            "chain": "norm_quantize_linear (qkv), quantize_linear (o+residual), norm_quantize_linear_swiglu "
-                     "(GEMV + row tail), down+residual; lm_head"}
+            "launches": 4 * synth.LAYERS + 3,
+            "chain": "norm_quantize_linear (qkv), quantize_linear (o+residual), norm_quantize_mlp "
+                     "(SwiGLU GEMV with the norm folded in, down+residual GEMV with the act row tail folded in); "
+                     "lm_head"}
         log(f"decode chain, fused producers: {ms * 1e3:.1f} us "
             f"({extras['decode_chain_fused_producers']['GB/s']} GB/s)")
         # latency-bound producers at M = 1: per call in a graph of 100

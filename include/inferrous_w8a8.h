@@ -317,6 +317,38 @@ int w8a8_norm_quantize_linear_swiglu(void *stream, const float *x,
                                      int8_t *q_out, float *scales_out,
                                      int out_dtype);
 
+/* The decode MLP block at M = 1 in two launches: norm_quantize of one
+ * 4096-wide f32 row, the SwiGLU projection of its codes (K = 4096), then
+ * quantize_with_max of act and the down projection (K = 12288) with an
+ * optional residual -- the reference's src/gpu.rs:713 (norm_quantize),
+ * :724-745 (linear_swiglu) and :775-786 (linear_residual, which runs
+ * quantize_with_max at :377-389 before its kernel).  No counterpart in the
+ * reference as one call.  The first launch is w8a8_norm_quantize_linear_swiglu's
+ * GEMV; the act row tail (maximum fold, quantize_with_max) runs inside the
+ * down GEMV, every workgroup recomputing the row's codes.  Bit-identical to
+ * w8a8_norm_quantize_linear_swiglu (with q_out / scales_out) followed by
+ * w8a8_linear_residual, or w8a8_linear without a residual, on those codes:
+ *   q[4096], scale[1], out_norm[4096] (optional), gate / up / act[n_ff] in
+ *   act_dtype (F32 or BF16) as w8a8_norm_quantize_linear_swiglu writes them;
+ *   maxima[0] (required): reset by the norm, then act's maximum folded in;
+ *   q_act[n_ff] (16-byte aligned) and scale_act[1] (both or neither): act's
+ *   codes and scale;
+ *   out[n] (required) and, with residual[n] (f32), combined[n] =
+ *   bf16(RN(residual + out)), in out_dtype (F32 or BF16), for
+ *   w_down / ws_down [n, n_ff].
+ * n_ff must be 12288; n >= 1.  x and gain must not overlap any output, and
+ * act must not overlap maxima, q_act, scale_act, out or combined. */
+int w8a8_norm_quantize_mlp(void *stream, const float *x, const float *gain,
+                           float *out_norm, int8_t *q, float *scale,
+                           const int8_t *w_gate, const float *ws_gate,
+                           const int8_t *w_up, const float *ws_up,
+                           size_t n_ff, void *gate, void *up, void *act,
+                           int act_dtype, uint32_t *maxima, int8_t *q_act,
+                           float *scale_act, const int8_t *w_down,
+                           const float *ws_down, size_t n,
+                           const float *residual, void *out, void *combined,
+                           int out_dtype);
+
 /* quantize of one f32 row of width 4096 (as w8a8_quantize with rows = 1)
  * followed by linear or linear_residual of its codes at M = 1, in one
  * launch: the reference's host linear_residual at decode (src/gpu.rs:364-415:

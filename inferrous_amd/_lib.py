@@ -71,6 +71,7 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_norm_quantize_linear": (I, [P, P, P, P, P, P, P, P, P, S, P, P, P, I]),
     "w8a8_quantize_linear": (I, [P, P, U32, P, P, P, P, P, S, P, P, P, I]),
     "w8a8_norm_quantize_linear_swiglu": (I, [P, P, P, P, P, P, P, P, P, P, S, P, P, P, P, P, P, I]),
+    "w8a8_norm_quantize_mlp": (I, [P, P, P, P, P, P, P, P, P, P, S, P, P, P, I, P, P, P, P, P, S, P, P, P, I]),
     "w8a8_swiglu": (I, [P, P, P, S, U32, P, P, I]),
     "w8a8_select_workspace_bytes": (S, [S]),
     "w8a8_select_token": (I, [P, P, S, P, P, S]),

@@ -76,6 +76,7 @@ int check_linear(const int8_t* q, const float* asc, size_t m, const int8_t* w, c
 // (kDot4MaxM).
 constexpr size_t kDot4MaxM = 4;
 constexpr size_t kDot4AutoMaxM = 2;
+constexpr size_t kRowtailWidthAbi = 12288;  // the down projection's K (the MLP width)
 
 static int auto_path(size_t m, size_t n, uint32_t k, size_t workspace_bytes) {
   if (m <= kDot4AutoMaxM) return W8A8_PATH_DOT4;
@@ -770,7 +771,77 @@ int w8a8_norm_quantize_linear_swiglu(void* stream, const float* x, const float* 
   a.maxima = maxima;
   a.q_out = q_out;
   a.scales_out = scales_out;
-  return hip_status(launch_gemv_swiglu_norm((hipStream_t)stream, p, a));
+  return hip_status(launch_gemv_swiglu_norm((hipStream_t)stream, p, a, true));
+}
+
+int w8a8_norm_quantize_mlp(void* stream, const float* x, const float* gain, float* out_norm, int8_t* q, float* scale,
+                           const int8_t* w_gate, const float* ws_gate, const int8_t* w_up, const float* ws_up,
+                           size_t n_ff, void* gate, void* up, void* act, int act_dtype, uint32_t* maxima,
+                           int8_t* q_act, float* scale_act, const int8_t* w_down, const float* ws_down, size_t n,
+                           const float* residual, void* out, void* combined, int out_dtype) {
+  if ((act_dtype != W8A8_OUT_F32 && act_dtype != W8A8_OUT_BF16) ||
+      (out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16))
+    return W8A8_EARG;
+  if (n_ff != kRowtailWidthAbi || n == 0 || n > kU32Max) return W8A8_ESHAPE;
+  if (!x || !gain || !q || !scale || !w_gate || !ws_gate || !w_up || !ws_up || !gate || !up || !act || !maxima ||
+      !w_down || !ws_down || !out)
+    return W8A8_ENULL;
+  if ((q_act == nullptr) != (scale_act == nullptr) || (residual == nullptr) != (combined == nullptr))
+    return W8A8_ENULL;
+  const int aa = out_align(act_dtype), oa = out_align(out_dtype);
+  if (!al(x, 4) || !al(gain, 4) || !al(out_norm, 4) || !al(q, 16) || !al(scale, 4) || !al(w_gate, 16) ||
+      !al(ws_gate, 4) || !al(w_up, 16) || !al(ws_up, 4) || !al(gate, aa) || !al(up, aa) || !al(act, aa) ||
+      !al(maxima, 4) || !al(q_act, 16) || !al(scale_act, 4) || !al(w_down, 16) || !al(ws_down, 4) ||
+      !al(residual, 4) || !al(out, oa) || !al(combined, oa))
+    return W8A8_EALIGN;
+  const size_t ab = n_ff * (size_t)aa, ob = n * (size_t)oa;
+  const struct {
+    const void* p;
+    size_t bytes;
+  } outs[] = {{out_norm, 4096 * 4}, {q, 4096},      {scale, 4}, {gate, ab}, {up, ab},       {act, ab},
+              {maxima, 4},          {q_act, n_ff}, {scale_act, 4}, {out, ob}, {combined, ob}};
+  for (const auto& o : outs)
+    if (overlaps(x, 4096 * 4, o.p, o.bytes) || overlaps(gain, 4096 * 4, o.p, o.bytes)) return W8A8_EARG;
+  // the down GEMV reads act in every workgroup while others write its outputs
+  for (size_t i = 6; i < sizeof(outs) / sizeof(outs[0]); ++i)
+    if (overlaps(act, ab, outs[i].p, outs[i].bytes)) return W8A8_EARG;
+  if (!ready()) return W8A8_EINIT;
+  hipStream_t st = (hipStream_t)stream;
+  ProduceArgs p{};
+  p.x = x;
+  p.gain = gain;
+  p.normed = out_norm;
+  p.q = q;
+  p.scale = scale;
+  p.maxima = maxima;
+  SwigluArgs a{};
+  a.k = 4096;
+  a.n = (uint32_t)n_ff;
+  a.wg = w_gate;
+  a.wsg = ws_gate;
+  a.wu = w_up;
+  a.wsu = ws_up;
+  a.gate = gate;
+  a.up = up;
+  a.act = act;
+  a.out_dtype = act_dtype;
+  a.maxima = maxima;
+  int s = hip_status(launch_gemv_swiglu_norm(st, p, a, false));
+  if (s != W8A8_OK) return s;
+  RowtailArgs d{};
+  d.act = act;
+  d.act_dtype = act_dtype;
+  d.maxima = maxima;
+  d.q_out = q_act;
+  d.scale_out = scale_act;
+  d.w = w_down;
+  d.ws = ws_down;
+  d.n = (uint32_t)n;
+  d.residual = residual;
+  d.out = out;
+  d.combined = combined;
+  d.out_dtype = out_dtype;
+  return hip_status(launch_gemv_rowtail(st, d));
 }
 
 int w8a8_quantize_linear(void* stream, const float* x, uint32_t width, int8_t* q, float* scale,

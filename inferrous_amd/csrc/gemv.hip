@@ -746,6 +746,88 @@ __global__ __launch_bounds__(kRowTailThreads) void swiglu_row_tail(const void* a
   }
 }
 
+// The SwiGLU row tail folded into the M = 1 down GEMV that consumes its
+// codes (gemv_m1_rowtail): swiglu_row_tail<true>'s work -- the act row's
+// largest bits(|act|) (NaN -> 0) folded into maxima[0], then
+// quantize_with_max (src/kernels.rs:453-475) with that maximum, s =
+// RN(from_bits(max(m0, row max)) / 127), q_j = round(RN(act_j / s)) -- then
+// linear / linear_residual (src/kernels.rs:577-618) on one matrix of
+// K = 12,288.  Every workgroup loads the act row ahead of its weights,
+// reduces the row maximum and quantizes the row with the row tail's own
+// expressions, so it holds the codes and scale the row tail would have
+// written; they reach the dot products through LDS.  m0 is maxima[0] as a
+// workgroup reads it: the call's value, or that value with the row maximum
+// folded in by workgroup 0's atomicMax -- max(m0, row max) is the same
+// either way.  Workgroup 0 also writes the codes and the scale (when asked
+// for) and folds the maximum, so the state after the call is the row
+// tail's.  Sixteen waves per workgroup, one row each: every workgroup
+// repeats the row's 12,288 divisions, so fewer, larger workgroups pay less
+// for them.  Measured on MI355X, graphs of 36 distinct-weight launches,
+// row tail + down with residual: 14.46 us per layer as two launches, 11.88
+// folded with 16 waves, 13.05 with 8, 16.85 with 4.
+constexpr int kRowtailWaves = 16;
+constexpr uint32_t kRowtailWidth = 12288;
+
+template <int EPI>
+__global__ __launch_bounds__(kRowtailWaves * kWave) void gemv_m1_rowtail(
+    const void* act, int act_dtype, uint32_t* maxima, const int8_t* w, const float* ws, uint32_t n, int dtype,
+    const float* residual, void* out, void* combined, int8_t* q_out, float* scale_out) {
+  constexpr int T = kRowtailWaves * kWave, PER = kRowtailWidth / T, KC = kRowtailWidth / 1024;
+  static_assert(kRowtailWidth % T == 0, "the row splits evenly over the workgroup");
+  __shared__ __attribute__((aligned(16))) int8_t qs[kRowtailWidth];
+  __shared__ uint32_t wmax[kRowtailWaves];
+  const int t = threadIdx.x, lane = t & 63, wv = wave_id();
+  // The producer's operands first: loads complete in issue order, so its
+  // math waits for them alone while the weights are in flight.
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] = load_val(act, t + (size_t)T * i, act_dtype);
+  const uint32_t m0 = maxima[0];
+  const uint32_t row0 = blockIdx.x * kRowtailWaves + wv;
+  const uint32_t erow = min(row0, n - 1);  // tail rows recompute the last row (n >= 1)
+  const float wsc = ws[erow];
+  const float resid = EPI == EPI_RESIDUAL ? residual[erow] : 0.f;
+  v4i wt[KC];
+  const int8_t* p = w + (size_t)erow * kRowtailWidth + lane * 16;
+#pragma unroll
+  for (int c = 0; c < KC; ++c) wt[c] = load_nt16(p + c * 1024);
+  uint32_t bits = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) bits = max(bits, abs_bits_no_nan(v[i]));
+  bits = wave_max_u32(bits);
+  if (lane == 0) wmax[wv] = bits;
+  __syncthreads();
+  uint32_t rmax = 0;
+#pragma unroll
+  for (int j = 0; j < kRowtailWaves; ++j) rmax = max(rmax, wmax[j]);
+  const float sc = __uint_as_float(max(m0, rmax)) / 127.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) qs[t + T * i] = round_i8(v[i] / sc);
+  if (blockIdx.x == 0 && t == 0) {
+    atomicMax(maxima, rmax);
+    if (scale_out) scale_out[0] = sc;
+  }
+  __syncthreads();
+  if (blockIdx.x == 0 && q_out && t < (int)(kRowtailWidth / 16))
+    *reinterpret_cast<v4i*>(q_out + t * 16) = *reinterpret_cast<const v4i*>(qs + t * 16);
+  v4i xq[KC];
+#pragma unroll
+  for (int c = 0; c < KC; ++c) xq[c] = *reinterpret_cast<const v4i*>(qs + c * 1024 + lane * 16);
+  int acc[1] = {0};
+#pragma unroll
+  for (int c = 0; c < KC; ++c) acc[0] = dot16(xq[c], wt[c], acc[0]);
+  const int total = reduce_to_lanes<1>(acc, lane);
+  const bool writer = lane == 0 && row0 < n;
+  // computed on every lane and pinned, as in gemv_m1_body
+  const float value = dequant(total, sc, wsc);
+  const float comb = EPI == EPI_RESIDUAL ? bf16_rne(resid + value) : 0.f;
+  asm volatile("" ::"v"(value), "v"(comb), "s"(dtype));
+  if (writer) {
+    if (out) store_out(out, row0, dtype, total, value);
+    if (EPI == EPI_RESIDUAL) store_out(combined, row0, dtype, total, comb);
+  }
+}
+
 // swiglu (src/kernels.rs:2172-2190): act = silu_mul(gate, up) elementwise
 // over rows x width (blockIdx.y = row); with maxima, each row's largest
 // |act| is published into maxima[row].
@@ -958,17 +1040,29 @@ hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {
   return hipGetLastError();
 }
 
-hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a) {
+hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a, bool row_tail) {
   if (a.n == 0 || a.k != 4096 || !a.maxima) return hipErrorInvalidValue;
   constexpr int RC = 2;
   const dim3 grid((a.n + RC * kGemvWaves - 1) / (RC * kGemvWaves));
   hipLaunchKernelGGL(gemv_swiglu_norm<RC>, grid, dim3(kGemvThreads), 0, st, p.x, p.gain, a.wg, a.wsg, a.wu, a.wsu,
                      a.n, a.out_dtype, a.gate, a.up, a.act, p.q, p.scale, p.maxima, p.normed);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !row_tail) return e;
   // the norm reset maxima[0] inside the GEMV; the row tail folds into it
   hipLaunchKernelGGL(swiglu_row_tail<true>, dim3(1), dim3(kRowTailThreads), 0, st, a.act, a.n, a.out_dtype,
                      a.maxima, a.q_out, a.scales_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_rowtail(hipStream_t st, const RowtailArgs& d) {
+  if (d.n == 0 || !d.maxima) return hipErrorInvalidValue;
+  const dim3 grid((d.n + kRowtailWaves - 1) / kRowtailWaves), block(kRowtailWaves * kWave);
+  if (d.residual)
+    hipLaunchKernelGGL(gemv_m1_rowtail<EPI_RESIDUAL>, grid, block, 0, st, d.act, d.act_dtype, d.maxima, d.w, d.ws,
+                       d.n, d.out_dtype, d.residual, d.out, d.combined, d.q_out, d.scale_out);
+  else
+    hipLaunchKernelGGL(gemv_m1_rowtail<EPI_PLAIN>, grid, block, 0, st, d.act, d.act_dtype, d.maxima, d.w, d.ws,
+                       d.n, d.out_dtype, nullptr, d.out, nullptr, d.q_out, d.scale_out);
   return hipGetLastError();
 }
 

@@ -109,7 +109,26 @@ hipError_t launch_gemv_produce(hipStream_t st, const ProduceArgs& p);
 // norm_quantize (p: x, gain, normed, q, scale; p.maxima == a.maxima) folded
 // into the M = 1 SwiGLU GEMV (a: k = 4096, maxima required), then the row
 // tail that folds the act maximum (and quantizes act when a.q_out is set).
-hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a);
+// row_tail: also run swiglu_row_tail<true> (maximum fold, and the codes when
+// a.q_out is set); without it maxima[0] is left as the norm reset it.
+hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a, bool row_tail);
+// The SwiGLU row tail folded into the M = 1, K = 12288 GEMV that consumes
+// its codes (gemv_m1_rowtail).
+struct RowtailArgs {
+  const void* act;   // [12288], act_dtype (F32 or BF16)
+  int act_dtype;
+  uint32_t* maxima;  // maxima[0]: read, the row maximum folded in
+  int8_t* q_out;     // optional: the row's codes
+  float* scale_out;  // optional: its scale
+  const int8_t* w;   // [n, 12288]
+  const float* ws;
+  uint32_t n;
+  const float* residual;  // optional, with combined
+  void* out;
+  void* combined;
+  int out_dtype;  // F32 or BF16
+};
+hipError_t launch_gemv_rowtail(hipStream_t st, const RowtailArgs& d);
 // Diagnostics: the one-matrix M = 1 GEMV with per-wave clock stamps.
 size_t gemv_timeline_waves(size_t n, uint32_t k);
 hipError_t launch_gemv_timeline(hipStream_t st, const int8_t* q, const float* asc, const int8_t* w,

@@ -196,6 +196,41 @@ def test_producer_linear_validation_precedes_device():
 
 
 @pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_norm_quantize_mlp_validation_precedes_device():
+    """w8a8_norm_quantize_mlp rejects malformed calls on the host: dtypes,
+    the MLP width (12288 only), required and paired pointers, alignment, and
+    outputs over x, the gains or (for the down GEMV's outputs) act."""
+    L = _lib.lib()
+    B = A + 0x100000  # outputs, clear of x [A, A + 16 KiB) and gain [A + 16 KiB, A + 32 KiB)
+
+    def mlp(**kw):
+        a = dict(x=A, gain=A + 0x4000, norm=None, q=B + 0x8000, sc=B + 0x9000, wg=B + 0x10000, sg=B + 0x20000,
+                 wu=B + 0x30000, su=B + 0x40000, nff=12288, gate=B + 0x50000, up=B + 0x60000, act=B + 0x70000,
+                 adt=_lib.OUT_F32, mx=B + 0x9010, qa=B + 0x80000, sa=B + 0x9020, wd=B + 0x90000, sd=B + 0xA0000,
+                 n=4096, res=B + 0xB0000, out=B + 0xC0000, comb=B + 0xD0000, dt=_lib.OUT_BF16)
+        a.update(kw)
+        return L.w8a8_norm_quantize_mlp(None, a["x"], a["gain"], a["norm"], a["q"], a["sc"], a["wg"], a["sg"],
+                                        a["wu"], a["su"], a["nff"], a["gate"], a["up"], a["act"], a["adt"], a["mx"],
+                                        a["qa"], a["sa"], a["wd"], a["sd"], a["n"], a["res"], a["out"], a["comb"],
+                                        a["dt"])
+
+    assert mlp() == _lib.EINIT
+    assert mlp(qa=None, sa=None, res=None, comb=None, norm=B) == _lib.EINIT
+    assert mlp(adt=_lib.OUT_I32) == _lib.EARG and mlp(dt=_lib.OUT_I32) == _lib.EARG and mlp(dt=9) == _lib.EARG
+    assert mlp(nff=4096) == _lib.ESHAPE and mlp(nff=12289) == _lib.ESHAPE
+    assert mlp(n=0) == _lib.ESHAPE and mlp(n=1 << 33) == _lib.ESHAPE
+    assert mlp(mx=None) == _lib.ENULL and mlp(out=None) == _lib.ENULL and mlp(wd=None) == _lib.ENULL
+    assert mlp(sa=None) == _lib.ENULL                  # q_act and scale_act go together
+    assert mlp(comb=None) == _lib.ENULL                # a residual needs combined
+    assert mlp(qa=B + 0x80008) == _lib.EALIGN and mlp(wd=B + 0x90004) == _lib.EALIGN
+    assert mlp(act=B + 0x70002) == _lib.EALIGN and mlp(out=B + 0xC0001) == _lib.EALIGN
+    assert mlp(act=A + 0x100) == _lib.EARG             # act over x
+    assert mlp(out=A + 0x4000) == _lib.EARG            # out over the gains
+    assert mlp(out=B + 0x70000 + 4 * 12000) == _lib.EARG   # out over act, read by every workgroup
+    assert mlp(mx=B + 0x70010) == _lib.EARG            # maxima over act
+
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
 def test_linear_validation_precedes_device():
     assert lin() == _lib.EINIT                       # well formed: stops at init
     assert lin(k=4095) == _lib.ESHAPE                # k % 16

@@ -3,7 +3,10 @@
 linear / linear_residual) and `w8a8_quantize_linear` (quantize,
 src/kernels.rs:433-451, then the same), one launch each, and
 `w8a8_norm_quantize_linear_swiglu` (norm_quantize, then linear_swiglu,
-src/kernels.rs:619-695, and optionally the act's quantize_with_max).
+src/kernels.rs:619-695, and optionally the act's quantize_with_max), and
+`w8a8_norm_quantize_mlp` (that GEMV, then the act's row tail --
+maximum fold and quantize_with_max, src/kernels.rs:453-475 -- folded into the
+down GEMV with its residual).
 
 Every workgroup recomputes the row's codes with the producer's arithmetic, so
 every output must equal the two-call sequence bit for bit: the codes, the
@@ -299,3 +302,148 @@ def test_norm_swiglu_matches_calls(env, quantize, dtype, n, kind):
         acc, of, ob = oracle.linear(wq.reshape(1, -1), wsc, wg, sg, 4096, threads=8)
         want_gate = ob if dtype == np.uint16 else of
         assert same_bits(folded["gate"], want_gate), "gate against the oracle"
+
+
+def run_mlp_both(env, x, gain, wg, sg, wu, su, wd, sd, resid, act_dtype, out_dtype, optional=True):
+    """(separate calls, folded call): norm_quantize_linear_swiglu with the
+    act's codes, then linear_residual (linear without a residual) on them,
+    against norm_quantize_mlp."""
+    _, mod, s = env
+    n_ff, n = sg.size, sd.size
+    xb, gb = dev(s, x), dev(s, gain)
+    wgb, sgb, wub, sub, wdb, sdb = dev(s, wg), dev(s, sg), dev(s, wu), dev(s, su), dev(s, wd), dev(s, sd)
+    rb = dev(s, resid) if resid is not None else None
+    res = {}
+    for mode in ("calls", "folded"):
+        q = DeviceBuffer.zeroed(s, 4096, np.int8)
+        sc = DeviceBuffer.zeroed(s, 1, np.float32)
+        nb = DeviceBuffer.zeroed(s, 4096, np.float32)
+        mx = dev(s, np.array([JUNK], np.uint32))
+        gate, up, act = (DeviceBuffer.zeroed(s, n_ff, act_dtype) for _ in range(3))
+        qa = DeviceBuffer.zeroed(s, n_ff, np.int8)
+        sa = DeviceBuffer.zeroed(s, 1, np.float32)
+        out = DeviceBuffer.zeroed(s, n, out_dtype)
+        comb = DeviceBuffer.zeroed(s, n, out_dtype) if resid is not None else None
+        if mode == "calls":
+            mod.norm_quantize_linear_swiglu(s, None, xb, gb, nb, q, sc, wgb, sgb, gate, wub, sub, up, act, mx,
+                                            qa, sa)
+            if resid is not None:
+                mod.linear_residual(s, None, qa, sa, wdb, sdb, n_ff, rb, out, comb)
+            else:
+                mod.linear(s, None, qa, sa, wdb, sdb, n_ff, out)
+        else:
+            mod.norm_quantize_mlp(s, None, xb, gb, nb if optional else None, q, sc, wgb, sgb, gate, wub, sub, up,
+                                  act, mx, wdb, sdb, out, rb, comb, qa if optional else None,
+                                  sa if optional else None)
+        s.synchronize()
+        res[mode] = dict(q=q.to_host_vec(s), sc=sc.to_host_vec(s), normed=nb.to_host_vec(s),
+                         mx=mx.to_host_vec(s), gate=gate.to_host_vec(s), up=up.to_host_vec(s),
+                         act=act.to_host_vec(s), qa=qa.to_host_vec(s), sa=sa.to_host_vec(s),
+                         out=out.to_host_vec(s), comb=comb.to_host_vec(s) if comb is not None else None)
+    return res["calls"], res["folded"]
+
+
+def mlp_weights(rng, n):
+    wg = rng.integers(-127, 128, (12288, 4096), dtype=np.int8)
+    wu = rng.integers(-127, 128, (12288, 4096), dtype=np.int8)
+    sg = (rng.random(12288) / 64 + 1e-4).astype(F32)
+    su = (rng.random(12288) / 64 + 1e-4).astype(F32)
+    wd = rng.integers(-127, 128, (n, 12288), dtype=np.int8)
+    sd = (rng.random(n) / 64 + 1e-4).astype(F32)
+    return wg, sg, wu, su, wd, sd
+
+
+@pytest.mark.parametrize("act_dtype,out_dtype,res", [(np.float32, np.uint16, True), (np.uint16, np.uint16, True),
+                                                     (np.float32, np.float32, True), (np.uint16, np.float32, False)])
+@pytest.mark.parametrize("n,kind", [(4096, "normal"), (1000, "normal"), (1, "normal"), (4096, "zero"),
+                                    (4096, "nan")])
+def test_norm_mlp_matches_calls(env, act_dtype, out_dtype, res, n, kind):
+    """The MLP block in two launches against norm_quantize_linear_swiglu
+    (with the act's codes) then linear_residual / linear: the norm's codes,
+    scale and row, gate / up / act, the maximum (reset by the norm, then the
+    act maximum folded in by the down GEMV's first workgroup), the act's
+    codes and scale, out and combined, bit for bit.  n = 1000 and 1 leave a
+    partly empty last 16-row workgroup (its rows clamped, not stored); the
+    zero row gives an all-zero act (scale from the floor), the NaN row NaN
+    gate / up / act (the maximum skips NaN).  The down outputs are also
+    checked against the oracle's quantize_with_max and linear."""
+    print(f"norm mlp n={n} {kind} act={np.dtype(act_dtype).name} out={np.dtype(out_dtype).name} res={res}",
+          flush=True)
+    rng = np.random.default_rng(n * 3 + len(kind) + (1 if res else 0))
+    x = make_row(rng, kind)
+    gain = (1 + 0.3 * rng.standard_normal(4096)).astype(F32)
+    wg, sg, wu, su, wd, sd = mlp_weights(rng, n)
+    resid = oracle.bf16_rne(rng.standard_normal(n).astype(F32)) if res else None
+    calls, folded = run_mlp_both(env, x, gain, wg, sg, wu, su, wd, sd, resid, act_dtype, out_dtype)
+    for key in ("q", "sc", "normed", "mx", "gate", "up", "act", "qa", "sa", "out") + (("comb",) if res else ()):
+        assert nan_same(folded[key], calls[key]), key
+    if kind != "nan":
+        act = folded["act"]
+        act32 = (act.astype(np.uint32) << 16).view(F32) if act_dtype == np.uint16 else act
+        wq, wsc = oracle.quantize_with_max(act32, 12288, folded["mx"])
+        assert np.array_equal(folded["qa"], wq) and np.array_equal(bits(folded["sa"]), bits(wsc))
+        acc, of, ob = oracle.linear(wq.reshape(1, -1), wsc, wd, sd, 12288, threads=8)
+        assert same_bits(folded["out"], ob if out_dtype == np.uint16 else of), "out against the oracle"
+        if res:
+            want = bits(oracle.residual(resid, of))
+            want = (want >> 16).astype(np.uint16) if out_dtype == np.uint16 else want.view(F32)
+            assert same_bits(folded["comb"], want), "combined against the oracle"
+
+
+def test_norm_mlp_optional_outputs(env):
+    """Without the normalised row and the act's codes / scale the required
+    outputs are unchanged."""
+    rng = np.random.default_rng(41)
+    x = make_row(rng)
+    gain = (1 + 0.3 * rng.standard_normal(4096)).astype(F32)
+    wg, sg, wu, su, wd, sd = mlp_weights(rng, 4096)
+    resid = oracle.bf16_rne(rng.standard_normal(4096).astype(F32))
+    calls, folded = run_mlp_both(env, x, gain, wg, sg, wu, su, wd, sd, resid, np.float32, np.uint16,
+                                 optional=False)
+    for key in ("q", "sc", "mx", "gate", "up", "act", "out", "comb"):
+        assert nan_same(folded[key], calls[key]), key
+
+
+def test_norm_mlp_graph_replay(env):
+    """The MLP block captured in a graph: every replay reproduces the eager
+    result (maxima restored to junk between replays, outputs cleared), with
+    eager work between the replays."""
+    _, mod, s = env
+    rng = np.random.default_rng(43)
+    x = make_row(rng)
+    gain = (1 + 0.3 * rng.standard_normal(4096)).astype(F32)
+    n = 4096
+    wg, sg, wu, su, wd, sd = mlp_weights(rng, n)
+    resid = oracle.bf16_rne(rng.standard_normal(n).astype(F32))
+    xb, gb, rb = dev(s, x), dev(s, gain), dev(s, resid)
+    wgb, sgb, wub, sub, wdb, sdb = dev(s, wg), dev(s, sg), dev(s, wu), dev(s, su), dev(s, wd), dev(s, sd)
+    q = DeviceBuffer.zeroed(s, 4096, np.int8)
+    sc = DeviceBuffer.zeroed(s, 1, np.float32)
+    mx = dev(s, np.array([JUNK], np.uint32))
+    gate, up, act = (DeviceBuffer.zeroed(s, 12288, np.float32) for _ in range(3))
+    qa = DeviceBuffer.zeroed(s, 12288, np.int8)
+    sa = DeviceBuffer.zeroed(s, 1, np.float32)
+    out = DeviceBuffer.zeroed(s, n, np.uint16)
+    comb = DeviceBuffer.zeroed(s, n, np.uint16)
+
+    def block():
+        mod.norm_quantize_mlp(s, None, xb, gb, None, q, sc, wgb, sgb, gate, wub, sub, up, act, mx, wdb, sdb, out,
+                              rb, comb, qa, sa)
+
+    bufs = (q, sc, mx, gate, up, act, qa, sa, out, comb)
+    block()
+    s.synchronize()
+    want = [b.to_host_vec(s) for b in bufs]
+    g = Graph(s)
+    with g:
+        block()
+    for _ in range(3):
+        for b in bufs:
+            b.fill_zero(s)
+        mx.copy_from_host(s, np.array([JUNK], np.uint32))
+        s.synchronize()
+        g.launch()
+        s.synchronize()
+        got = [b.to_host_vec(s) for b in bufs]
+        for a, b in zip(got, want):
+            assert nan_same(a, b)
