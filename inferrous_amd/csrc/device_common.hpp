@@ -31,6 +31,23 @@ __device__ __forceinline__ int8_t round_i8(float v) {
   return (int8_t)(int)__builtin_rintf(v);  // v_rndne_f32: ties to even
 }
 
+// round_i8(RN(v / s)) from r = RN(1 / s), for a scale s = RN(m / 127) of a
+// maximum m >= |v| (so |v / s| <= 128): the code of quantize
+// (src/kernels.rs:441-449) without a division per element.  y = RN(v * r)
+// lies within |v / s| * 2^-23 <= 2^-16 of v / s, and RN(v / s) within 2^-18
+// of it, so y and RN(v / s) are less than 2^-15 apart: unless y is within
+// that distance of a half-integer they round to the same integer (and the
+// clamp to +-127 commutes with the rounding, its bounds being integers).
+// Those cases, and NaN, take the division itself.  About 2^-11 of uniformly
+// spread values do.  Used where a workgroup recomputes a row's codes that
+// another kernel would compute once (the folded producers).
+__device__ __forceinline__ int8_t quant_code(float v, float s, float r) {
+  const float y = v * r;
+  const float ry = __builtin_rintf(y);
+  if (__builtin_fabsf(y - ry) < 0.5f - 0x1p-12f) return (int8_t)(int)__builtin_fminf(__builtin_fmaxf(ry, -127.0f), 127.0f);
+  return round_i8(v / s);
+}
+
 // |x| as ordered bits with NaN mapped to 0 (f32::max ignores NaN,
 // src/kernels.rs:133-139); non-negative floats order like unsigned ints.
 __device__ __forceinline__ uint32_t abs_bits_no_nan(float x) {

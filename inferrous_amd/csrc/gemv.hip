@@ -336,8 +336,9 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_m1_timed(const int8_t* w
 // quantize (src/kernels.rs:433-451) of one 4096-wide f32 row, then linear /
 // linear_residual (src/kernels.rs:577-618, :807-845) on one matrix.  Every
 // workgroup loads the row (and the gains) ahead of its weight stream and
-// recomputes the row's codes and scale with the producer's own arithmetic
-// and order, so every workgroup holds the same bits the producer kernel
+// recomputes the row's scale with the producer's own arithmetic and order,
+// and its codes with quant_code (the same integers as the producer's
+// division), so every workgroup holds the same bits the producer kernel
 // would have written; they reach the dot products through LDS.  Workgroup 0
 // also writes the producer's outputs (codes, scale, the normalised row when
 // asked for, the maxima reset).  One launch instead of two: measured on
@@ -375,9 +376,9 @@ __device__ __forceinline__ float producer_codes(float (&v)[16], const float (&g)
     for (int i = 0; i < 16; ++i) mb = max(mb, abs_bits_no_nan(v[i]));
   }
   mb = block_max_256(mb, L.red);
-  const float sc = __uint_as_float(mb) / 127.0f;
+  const float sc = __uint_as_float(mb) / 127.0f, rc = 1.0f / sc;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) L.qs[t + 256 * i] = round_i8(v[i] / sc);
+  for (int i = 0; i < 16; ++i) L.qs[t + 256 * i] = quant_code(v[i], sc, rc);
   return sc;
 }
 
@@ -753,9 +754,10 @@ __global__ __launch_bounds__(kRowTailThreads) void swiglu_row_tail(const void* a
 // RN(from_bits(max(m0, row max)) / 127), q_j = round(RN(act_j / s)) -- then
 // linear / linear_residual (src/kernels.rs:577-618) on one matrix of
 // K = 12,288.  Every workgroup loads the act row ahead of its weights,
-// reduces the row maximum and quantizes the row with the row tail's own
-// expressions, so it holds the codes and scale the row tail would have
-// written; they reach the dot products through LDS.  m0 is maxima[0] as a
+// reduces the row maximum with the row tail's expressions and quantizes the
+// row to the row tail's codes (quant_code: the same integers without a
+// division per element), so it holds the codes and scale the row tail would
+// have written; they reach the dot products through LDS.  m0 is maxima[0] as a
 // workgroup reads it: the call's value, or that value with the row maximum
 // folded in by workgroup 0's atomicMax -- max(m0, row max) is the same
 // either way.  Workgroup 0 also writes the codes and the scale (when asked
@@ -800,9 +802,9 @@ __global__ __launch_bounds__(kRowtailWaves * kWave) void gemv_m1_rowtail(
   uint32_t rmax = 0;
 #pragma unroll
   for (int j = 0; j < kRowtailWaves; ++j) rmax = max(rmax, wmax[j]);
-  const float sc = __uint_as_float(max(m0, rmax)) / 127.0f;
+  const float sc = __uint_as_float(max(m0, rmax)) / 127.0f, rc = 1.0f / sc;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) qs[t + T * i] = round_i8(v[i] / sc);
+  for (int i = 0; i < PER; ++i) qs[t + T * i] = quant_code(v[i], sc, rc);
   if (blockIdx.x == 0 && t == 0) {
     atomicMax(maxima, rmax);
     if (scale_out) scale_out[0] = sc;
