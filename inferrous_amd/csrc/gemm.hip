@@ -1034,9 +1034,16 @@ static void launch_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits, 
 template <bool NT>
 static hipError_t launch_splitk_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits) {
   if (splits < 1 || splits > kMaxSplits) return hipErrorInvalidValue;
-  // 8 columns per thread when every row of every operand starts 16-byte
-  // aligned (n % 8 == 0 and aligned bases); 4 otherwise
-  const bool wide = a.n % 8 == 0 && aligned16(a.partials) && aligned16(a.out) &&
+  // 8 columns per thread above M = 200 when every row of every operand
+  // starts 16-byte aligned (n % 8 == 0 and aligned bases); 4 otherwise.  The
+  // epilogue is latency-bound: up to M = 200 twice the threads with half the
+  // loads each finish sooner.  Measured on MI355X, graphs of 16
+  // distinct-weight launches, GEMM + epilogue, 8 -> 4 columns: M = 64 o
+  // 10.3 -> 9.7 us, M = 100 qkv 14.4 -> 13.5, M = 129 qkv 15.6-15.8 -> 14.9,
+  // o 13.5-13.9 -> 13.1, down 22.6-24.1 -> 22.0, M = 200 qkv 18.7 -> 17.7;
+  // but M = 255 o 15.9-16.1 -> 17.1, and level on gemm_dma's split route at
+  // M = 300 and 512.
+  const bool wide = a.m > 200 && a.n % 8 == 0 && aligned16(a.partials) && aligned16(a.out) &&
                     (a.out_dtype == W8A8_OUT_I32 || aligned16(a.ws)) &&
                     (!a.residual || (aligned16(a.residual) && aligned16(a.combined)));
   if (a.out_dtype == W8A8_OUT_I32)

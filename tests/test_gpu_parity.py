@@ -584,7 +584,8 @@ def test_errors_raise_not_fall_back(env):
                                    (100, 96, 12288), (255, 1024, 4096), (100, 4096, 12288), (65, 4100, 12288),
                                    (128, 4096, 4096),
                                    (129, 4100, 4096), (64, 4100, 12288), (512, 4100, 12288),
-                                   (16, 4100, 12288), (100, 1024, 4096), (3, 4100, 12288), (7, 1024, 8192)])
+                                   (16, 4100, 12288), (100, 1024, 4096), (3, 4100, 12288), (7, 1024, 8192),
+                                   (255, 4096, 4096)])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     """w8a8_linear_ex with a workspace (split-K partials + exact i32 epilogue)
@@ -592,11 +593,13 @@ def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     second call with the same workspace, which carries nothing between calls.
     Below M = 16 only K >= 8192 splits (3 x 4100 x 12288 under AUTO's MFMA
     route from M = 3, 7 x 1024 x 8192).
-    The shapes cover both slab policies with the 16-byte and the 4-column
-    epilogue each: streamed (gemm_tall from 3 MiB of slabs, e.g. 129 x 4096 x
-    4096 and 64 x 4100 x 12288) and plain (smaller gemm_tall sets such as
-    16 x 4100 x 12288, 100 x 96 x 12288 and 100 x 1024 x 4096, and gemm_dma's
-    split route above M = 256: 512 x 4096 x 12288 and 512 x 4100 x 12288)."""
+    The shapes cover both slab policies with the 16-byte epilogue (M > 200,
+    N % 8 == 0) and the 4-column one: streamed (gemm_tall from 3 MiB of
+    slabs: 129 x 4096 x 4096 and 64 x 4100 x 12288 on 4 columns, 255 x 4096
+    x 4096 on 16 bytes) and plain (smaller gemm_tall sets such as 16 x 4100 x
+    12288, 100 x 96 x 12288 and 100 x 1024 x 4096, and gemm_dma's split route
+    above M = 256: 512 x 4096 x 12288 on 16 bytes, 512 x 4100 x 12288 on 4
+    columns)."""
     from inferrous_amd import _lib
     ctx, mod, s = env
     print(f"split-K m={m} n={n} k={k} {np.dtype(dtype).name} res={res}", flush=True)
