@@ -1118,25 +1118,21 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
     uint32_t splits;
     if (tall_plan(a.m, a.n, a.k, tile, splits, ma) &&
         (splits == 1 || (a.partials && a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t)))) {
-      // Ring depths: the unsplit wide-N tiles (96 columns, the whole K) look
-      // further ahead on the weights; the split routes, a quarter of K each,
-      // run four and four.  Measured on MI355X, graphs of 16 distinct-weight
-      // launches, GEMM + epilogue, deeper rings -> 4 / 4: M = 16 qkv 10.25 ->
-      // 9.3 us, o 8.56 -> 8.24, down 13.7 -> 13.2; M = 64 qkv 11.6-11.8 ->
-      // 10.4, o 9.6-9.8 -> 8.8, down 15.4-16.0 -> 14.9 (from 4 / 8 and 8 / 8);
-      // M = 80 qkv 12.5 -> 11.6, down 18.7-19.5 -> 16.9; M = 100 qkv 13.2 ->
-      // 12.4-12.6, o 11.2 -> 10.4, down 19.6-19.8 -> 17.7-18.1; M = 129 qkv
-      // 14.7-14.8 -> 14.0-14.3, o 13.1-13.2 -> 12.4-12.6; M = 160 down level
-      // (from 4 / 6 and 5 / 5).  6 / 6 and 3 / 3 measured between the two.
-      if (splits > 1 && ma != 256)
-        return tile == 96 ? (ma == 64 ? launch_tall<96, 4, 4, 64>(st, a, splits)
-                                      : launch_tall<96, 4, 4, 160>(st, a, splits))
-                          : (ma == 64 ? launch_tall<64, 4, 4, 64>(st, a, splits)
-                                      : launch_tall<64, 4, 4, 160>(st, a, splits));
+      // Ring depths four and four for the 64- and 160-row tiles.  Measured on
+      // MI355X, graphs of 16 distinct-weight launches (split routes: GEMM +
+      // epilogue), from 8 / 8 and 4 / 8 (64 rows) and 5 / 5 and 4 / 6 (160
+      // rows): M = 16 qkv 10.25 -> 9.3 us, o 8.56 -> 8.24, down 13.7 -> 13.2,
+      // gate_up 18.1 -> 17.3; M = 64 qkv 11.6-11.8 -> 10.4, o 9.6-9.8 -> 8.8,
+      // down 15.4-16.0 -> 14.9, gate_up 19.7-20.0 -> 19.0-19.2; M = 80 down
+      // 18.7-19.5 -> 16.9; M = 100 qkv 13.2 -> 12.4-12.6, o 11.2 -> 10.4,
+      // down 19.6-19.8 -> 17.7-18.1; M = 129 qkv 14.7-14.8 -> 14.0-14.3, o
+      // 13.1-13.2 -> 12.4-12.6, gate_up 28.7-28.9 -> 27.0-28.1; M = 160 down
+      // level.  6 / 6, 5 / 5 and 3 / 3 measured in between.  The 256-row
+      // tile's 3 / 3 and 4 / 4 fill its LDS.
       if (ma == 64)
-        return tile == 96 ? launch_tall<96, 4, 8, 64>(st, a, splits) : launch_tall<64, 8, 8, 64>(st, a, splits);
+        return tile == 96 ? launch_tall<96, 4, 4, 64>(st, a, splits) : launch_tall<64, 4, 4, 64>(st, a, splits);
       if (ma == 160)
-        return tile == 96 ? launch_tall<96, 4, 6, 160>(st, a, splits) : launch_tall<64, 5, 5, 160>(st, a, splits);
+        return tile == 96 ? launch_tall<96, 4, 4, 160>(st, a, splits) : launch_tall<64, 4, 4, 160>(st, a, splits);
       return tile == 96 ? launch_tall<96, 3, 3, 256>(st, a, splits) : launch_tall<64, 4, 4, 256>(st, a, splits);
     }
   }
