@@ -1127,7 +1127,7 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
       // 18.7-19.5 -> 16.9; M = 100 qkv 13.2 -> 12.4-12.6, o 11.2 -> 10.4,
       // down 19.6-19.8 -> 17.7-18.1; M = 129 qkv 14.7-14.8 -> 14.0-14.3, o
       // 13.1-13.2 -> 12.4-12.6, gate_up 28.7-28.9 -> 27.0-28.1; M = 160 down
-      // level.  6 / 6, 5 / 5 and 3 / 3 measured in between.  The 256-row
+      // level.  6 / 6, 5 / 5, 4 / 5, 3 / 4 and 3 / 3 measured in between.  The 256-row
       // tile's 3 / 3 and 4 / 4 fill its LDS.
       if (ma == 64)
         return tile == 96 ? launch_tall<96, 4, 4, 64>(st, a, splits) : launch_tall<64, 4, 4, 64>(st, a, splits);
