@@ -795,16 +795,20 @@ int w8a8_norm_quantize_mlp(void* stream, const float* x, const float* gain, floa
       !al(residual, 4) || !al(out, oa) || !al(combined, oa))
     return W8A8_EALIGN;
   const size_t ab = n_ff * (size_t)aa, ob = n * (size_t)oa;
-  const struct {
+  struct Span {
     const void* p;
     size_t bytes;
-  } outs[] = {{out_norm, 4096 * 4}, {q, 4096},      {scale, 4}, {gate, ab}, {up, ab},       {act, ab},
-              {maxima, 4},          {q_act, n_ff}, {scale_act, 4}, {out, ob}, {combined, ob}};
-  for (const auto& o : outs)
+  };
+  // written by the SwiGLU GEMV, and by the down GEMV (which reads act in
+  // every workgroup while others write these)
+  const Span first[] = {{out_norm, 4096 * 4}, {q, 4096}, {scale, 4}, {gate, ab}, {up, ab}, {act, ab}};
+  const Span second[] = {{maxima, 4}, {q_act, n_ff}, {scale_act, 4}, {out, ob}, {combined, ob}};
+  for (const Span& o : first)
     if (overlaps(x, 4096 * 4, o.p, o.bytes) || overlaps(gain, 4096 * 4, o.p, o.bytes)) return W8A8_EARG;
-  // the down GEMV reads act in every workgroup while others write its outputs
-  for (size_t i = 6; i < sizeof(outs) / sizeof(outs[0]); ++i)
-    if (overlaps(act, ab, outs[i].p, outs[i].bytes)) return W8A8_EARG;
+  for (const Span& o : second)
+    if (overlaps(x, 4096 * 4, o.p, o.bytes) || overlaps(gain, 4096 * 4, o.p, o.bytes) ||
+        overlaps(act, ab, o.p, o.bytes))
+      return W8A8_EARG;
   if (!ready()) return W8A8_EINIT;
   hipStream_t st = (hipStream_t)stream;
   ProduceArgs p{};
