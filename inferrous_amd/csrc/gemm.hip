@@ -965,14 +965,15 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
 // with streamed slabs the split route also beats gemm_dma's split-K 2 on
 // qkv and o (qkv at M = 65 / 100 / 128 12.6 / 14.1 / 14.5 against
 // 13.2-13.3 / 14.6 / 15.5, o 10.9 / 11.6 / 12.7 against 12.0 / 12.7 / 13.2).
-// Below m = 16 the plan applies to the wide shapes and to long K only, where
-// it beats gemm_skinny (graphs of 16 distinct-weight launches, random
+// At small m the plan applies to the wide shapes and to long K at any m,
+// where it beats gemm_skinny (graphs of 16 distinct-weight launches, random
 // operands, m = 1..6: gate_up 17.9-18.1 against 21.2-24.0 us, down at
-// K = 12288 13.1-13.5 against 16.7-17.1).  On qkv and o at K = 4096 the
-// skinny kernel's split-K leads up to there: qkv at m = 1..6 / 8 / 12 / 16
-// / 24 8.3-9.1 / 9.5 / 10.6 / 11.5 / 14.1 us against 9.7-10.1 / 10.3 / 10.5
-// / 10.5 / 10.9, o 6.9-7.4 / 7.5 / 7.7 / 7.9 / 9.6 against 8.1-8.4 / 8.3 /
-// 8.5 / 8.7 / 9.0.
+// K = 12288 13.1-13.5 against 16.7-17.1).  At K = 4096 on narrow N the
+// skinny kernel (one workgroup per 16 columns) leads while its grid fits the
+// CUs once: o (4096 columns) at m = 2 / 4 / 8 / 12 / 16 / 24 7.1 / 7.2 /
+// 7.4 / 7.6 / 7.9 / 9.6 us against 7.8 / 7.8 / 8.0 / 8.0 / 8.2 / 9.0; qkv
+// (6144 columns) 8.4 / 8.8 / 9.6 / 10.5 / 11.5 against 8.6 / 8.8 / 9.0 /
+// 9.1 / 9.3, so it takes this plan from m = 8, o from m = 24.
 // Returns false when no plan applies (the gemm_dma or gemm_skinny routes
 // then run).  ma: the M tile (64, 160 or 256 rows).
 static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits, int& ma) {
@@ -985,7 +986,7 @@ static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& spl
     return true;
   }
   if (n % 4 != 0) return false;  // the split-K epilogue works on column quads
-  if (m < 16 && k < 8192) return false;
+  if (k < 8192 && (m < 8 || (m < 24 && (n + 15) / 16 <= 256))) return false;
   splits = (kt % 4 == 0 && kt / 4 >= 4) ? 4 : (kt % 2 == 0 && kt / 2 >= 4) ? 2 : 1;
   if (splits == 1) return false;
   bn = t96 * splits >= 224 ? 96 : 64;
