@@ -177,6 +177,34 @@ def test_linear_random_shapes(env, m):
             assert np.array_equal(ob.to_host_vec(s), outb), f"{op} bf16 m={m} n={n} k={k}"
 
 
+@pytest.mark.parametrize("m", [7, 8, 12, 23, 24])
+@pytest.mark.parametrize("n", [6144, 4096])
+def test_small_batch_qkv_o_routes(env, m, n):
+    """The small-batch boundary at K = 4096 on narrow N: the skinny kernel
+    below M = 8 (and below M = 24 for N <= 4096), the one-M-tile split-K
+    route above (with the module's workspace).  AUTO and the forced MFMA
+    family equal the oracle bit for bit on both sides of each boundary."""
+    ctx, mod, s = env
+    k = 4096
+    print(f"small-batch route m={m} n={n}", flush=True)
+    rng = np.random.default_rng(7000 + m + n)
+    q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    q[-1] = 127
+    w[-1] = -127
+    asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+    ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+    acc, out, outb = oracle.linear(q, asc, w, ws, k, threads=8)
+    dq, da, dw, dws = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws)
+    for op in ("linear", "linear_mfma"):
+        o32 = DeviceBuffer.zeroed(s, m * n, np.int32)
+        getattr(mod, op)(s, None, dq, da, dw, dws, k, o32)
+        assert np.array_equal(o32.to_host_vec(s), acc), f"{op} acc"
+        ob = DeviceBuffer.zeroed(s, m * n, np.uint16)
+        getattr(mod, op)(s, None, dq, da, dw, dws, k, ob)
+        assert np.array_equal(ob.to_host_vec(s), outb), f"{op} bf16"
+
+
 def test_linear_residual(env, fixtures):
     ctx, mod, s = env
     for c in fixtures.cases("linear"):
