@@ -1128,13 +1128,18 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
       // 18.7-19.5 -> 16.9; M = 100 qkv 13.2 -> 12.4-12.6, o 11.2 -> 10.4,
       // down 19.6-19.8 -> 17.7-18.1; M = 129 qkv 14.7-14.8 -> 14.0-14.3, o
       // 13.1-13.2 -> 12.4-12.6, gate_up 28.7-28.9 -> 27.0-28.1; M = 160 down
-      // level.  6 / 6, 5 / 5, 4 / 5, 3 / 4 and 3 / 3 measured in between.  The 256-row
-      // tile's 3 / 3 and 4 / 4 fill its LDS.
+      // level.  6 / 6, 5 / 5, 4 / 5, 3 / 4 and 3 / 3 measured in between.  The
+      // 256-row tile: 2 / 4 for the unsplit 96-column tiles (gate_up at
+      // M = 200 33.7-35.1 -> 31.5-32.9 us, M = 255 37.6-37.9 -> 36.1-37.1
+      // from 3 / 3), 3 / 3 and 4 / 4 for the split routes (2 / 3, 2 / 4 and
+      // 3 / 4 level or slower there).
       if (ma == 64)
         return tile == 96 ? launch_tall<96, 4, 4, 64>(st, a, splits) : launch_tall<64, 4, 4, 64>(st, a, splits);
       if (ma == 160)
         return tile == 96 ? launch_tall<96, 4, 4, 160>(st, a, splits) : launch_tall<64, 4, 4, 160>(st, a, splits);
-      return tile == 96 ? launch_tall<96, 3, 3, 256>(st, a, splits) : launch_tall<64, 4, 4, 256>(st, a, splits);
+      if (tile == 96)
+        return splits > 1 ? launch_tall<96, 3, 3, 256>(st, a, splits) : launch_tall<96, 2, 4, 256>(st, a, splits);
+      return launch_tall<64, 4, 4, 256>(st, a, splits);
     }
   }
   if (a.m <= 16 && !wide) {
