@@ -203,6 +203,17 @@ int w8a8_linear_path(void *stream, const int8_t *q, const float *asc, size_t m,
  * workspace selects the unsplit kernels.  Calls sharing one workspace must
  * not overlap. */
 size_t w8a8_linear_workspace_bytes(size_t m, size_t n, uint32_t k);
+/* The same for one route: 0 for W8A8_PATH_DOT4, and for W8A8_PATH_AUTO
+ * where AUTO runs the dot4 GEMV whatever the workspace (m <= 2); the MFMA
+ * family's need otherwise.  Size a per-call workspace with this. */
+size_t w8a8_linear_workspace_bytes_path(size_t m, size_t n, uint32_t k, int path);
+/* The largest w8a8_linear_workspace_bytes(m, n, k) over m = 1 .. max_m.
+ * The need is not monotone in m: 6144 x 4096 needs 25.2 MB at m = 256 and
+ * none at m = 512, and 4096 x 12288 needs 16.8 MB at m = 256, 8.4 MB at
+ * m = 257 and 16.8 MB at m = 512.  A buffer shared by every batch size up
+ * to max_m is sized with this, taken over every projection shape the
+ * caller runs. */
+size_t w8a8_linear_workspace_bytes_upto(size_t max_m, size_t n, uint32_t k);
 int w8a8_linear_ex(void *stream, const int8_t *q, const float *asc, size_t m,
                    const int8_t *w, const float *ws, size_t n, uint32_t k,
                    const float *residual, void *out, void *combined,

@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_linear_residual": (I, [P, P, P, S, P, P, S, U32, P, P, P, I]),
     "w8a8_linear_grouped": (I, [P, P, P, S, U32, I, P, P, P, P, I]),
     "w8a8_linear_workspace_bytes": (S, [S, S, U32]),
+    "w8a8_linear_workspace_bytes_path": (S, [S, S, U32, I]),
+    "w8a8_linear_workspace_bytes_upto": (S, [S, S, U32]),
     "w8a8_norm_quantize": (I, [P, P, P, S, U32, P, P, P, P]),
     "w8a8_bf16_pack": (I, [P, S, P, P, P, S, P]),
     "w8a8_head_packed": (I, [P, P, S, P, P, P, S, S, P]),

@@ -519,6 +519,22 @@ size_t w8a8_linear_workspace_bytes(size_t m, size_t n, uint32_t k) {
   return gemm_workspace_bytes((uint32_t)m, (uint32_t)n, k);
 }
 
+size_t w8a8_linear_workspace_bytes_path(size_t m, size_t n, uint32_t k, int path) {
+  if (path == W8A8_PATH_DOT4) return 0;
+  if (path == W8A8_PATH_AUTO && m <= kDot4AutoMaxM) return 0;  // AUTO runs the dot4 GEMV there
+  if (path != W8A8_PATH_AUTO && path != W8A8_PATH_MFMA) return 0;
+  return w8a8_linear_workspace_bytes(m, n, k);
+}
+
+size_t w8a8_linear_workspace_bytes_upto(size_t max_m, size_t n, uint32_t k) {
+  // The split plans depend on M in both directions (gemm_tall's split-K
+  // slabs peak below M = 256 on narrow N), so take every M.
+  size_t most = 0;
+  if (max_m > kU32Max) max_m = kU32Max;
+  for (size_t m = 1; m <= max_m; ++m) most = std::max(most, w8a8_linear_workspace_bytes(m, n, k));
+  return most;
+}
+
 int w8a8_linear_ex(void* stream, const int8_t* q, const float* asc, size_t m, const int8_t* w,
                    const float* ws, size_t n, uint32_t k, const float* residual, void* out,
                    void* combined, int out_dtype, int path, void* workspace, size_t workspace_bytes) {

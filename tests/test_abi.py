@@ -458,6 +458,34 @@ def test_module_grouped_and_swiglu_check_operand_lengths():
                                    _fake(m * n - 1, np.int8), so)
 
 
+def test_module_argmax_and_quantize_with_max_check_operand_lengths():
+    """linear_argmax and linear_quantize_with_max refuse a weight matrix
+    shorter than N*K and an activation row shorter than K with ValueError,
+    before the library is called (a short buffer must never reach the
+    device as an out-of-bounds read)."""
+    import numpy as np
+
+    from inferrous_amd import LoadedModule
+    mod = LoadedModule(None)
+    k, n = 64, 8
+    asc, ws, tok = _fake(1, np.float32), _fake(n, np.float32), _fake(1, np.uint32)
+    good_w, short_w = _fake(n * k, np.int8), _fake(n * k - 1, np.int8)
+    with pytest.raises(ValueError, match="w has"):
+        mod.linear_argmax(None, _fake(k, np.int8), asc, short_w, ws, k, tok)
+    with pytest.raises(ValueError, match="q has"):
+        mod.linear_argmax(None, _fake(k - 16, np.int8), asc, good_w, ws, k, tok)
+    m = 2
+    x, q, sc = _fake(m * k, np.float32), _fake(m * k, np.int8), _fake(m, np.float32)
+    out = _fake(m * n, np.float32)
+    with pytest.raises(ValueError, match="w has"):
+        mod.linear_quantize_with_max(None, None, x, k, _fake(m, np.uint32), q, sc, short_w, ws, out)
+    with pytest.raises(ValueError, match="maxima has"):
+        mod.linear_quantize_with_max(None, None, x, k, _fake(m - 1, np.uint32), q, sc, good_w, ws, out)
+    with pytest.raises(ValueError, match="sizes do not match"):
+        mod.linear_quantize_with_max(None, None, x, k, _fake(m, np.uint32), _fake(m * k - 4, np.int8), sc,
+                                     good_w, ws, out)
+
+
 @pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
 def test_noalloc_argmax_validation():
     """Rows beyond the fixed key array are refused with ESHAPE before any
@@ -470,3 +498,26 @@ def test_noalloc_argmax_validation():
     assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, top, 4096, A + 2, None, 0) == _lib.EALIGN
     assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, top, 4096, A, A, 7) == _lib.EARG
     assert L.w8a8_linear_argmax_noalloc(None, A, A, A, A, 33, 4004, A, None, 0) == _lib.ESHAPE
+
+
+def test_workspace_queries_by_route_and_batch_range():
+    """The split-K workspace need depends on the route and is not monotone
+    in M: AUTO at M <= 2 runs the dot4 GEMV and needs nothing, DOT4 never
+    does, MFMA keeps the shape's need; the largest need over M = 1..512 for
+    qkv (6144 x 4096) sits at M = 256, where M = 512 needs none."""
+    L = _lib.lib()
+    down = (4096, 12288)
+    assert L.w8a8_linear_workspace_bytes(1, *down) > 0
+    assert L.w8a8_linear_workspace_bytes_path(1, *down, _lib.PATH_AUTO) == 0
+    assert L.w8a8_linear_workspace_bytes_path(2, *down, _lib.PATH_AUTO) == 0
+    assert L.w8a8_linear_workspace_bytes_path(3, *down, _lib.PATH_AUTO) == L.w8a8_linear_workspace_bytes(3, *down)
+    assert L.w8a8_linear_workspace_bytes_path(1, *down, _lib.PATH_MFMA) == L.w8a8_linear_workspace_bytes(1, *down)
+    assert L.w8a8_linear_workspace_bytes_path(64, *down, _lib.PATH_DOT4) == 0
+    assert L.w8a8_linear_workspace_bytes_path(64, *down, 7) == 0
+    qkv = (6144, 4096)
+    at256 = L.w8a8_linear_workspace_bytes(256, *qkv)
+    assert at256 == 4 * 256 * 6144 * 4 and L.w8a8_linear_workspace_bytes(512, *qkv) == 0
+    assert L.w8a8_linear_workspace_bytes_upto(512, *qkv) == at256
+    assert L.w8a8_linear_workspace_bytes_upto(512, *down) == max(
+        L.w8a8_linear_workspace_bytes(m, *down) for m in range(1, 513))
+    assert L.w8a8_linear_workspace_bytes_upto(0, *down) == 0

@@ -330,6 +330,7 @@ def test_decode_mlp_chain_combined_down_entry(env):
 
 
 @pytest.mark.parametrize("m,k,n,dtype", [(1, 4096, 12288, np.float32), (1, 4096, 12288, np.uint16),
+                                         (1, 4096, 20000, np.float32), (1, 4096, 20000, np.uint16),
                                          (1, 12288, 1000, np.float32), (1, 128, 33, np.uint16),
                                          (3, 4096, 4099, np.float32), (2, 1024, 5000, np.uint16)])
 def test_linear_swiglu_quantize_matches_separate_calls(env, m, k, n, dtype):
@@ -339,7 +340,8 @@ def test_linear_swiglu_quantize_matches_separate_calls(env, m, k, n, dtype):
     act with the folded maxima (the oracle restatement of
     src/kernels.rs:453-475) -- at M = 1 on the fused GEMV (one workgroup
     folds the maximum and quantizes), and on the grouped / MFMA route.
-    The maxima start at a reset floor on one row and at a large stale value
+    n = 20000 at M = 1 exceeds the row tail's register-held width (16,384),
+    so its re-reading fold and quantize loops run too.  The maxima start at a reset floor on one row and at a large stale value
     on another, so the fold (not the row maximum) sets the scale."""
     ctx, mod, s = env
     print(f"linear_swiglu_quantize m={m} k={k} n={n} dtype={np.dtype(dtype).name}", flush=True)
