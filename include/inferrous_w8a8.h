@@ -402,6 +402,64 @@ int w8a8_linear_argmax(void *stream, const int8_t *q, const float *asc,
                        uint32_t *token, void *logits, int logits_dtype,
                        void *workspace, size_t workspace_bytes);
 
+/* ------------------------------------------------------------ decode sequence
+ * A dependent sequence of M = 1 projections in one launch: the decode
+ * step's linear / linear_residual calls (src/kernels.rs:577-618, :807-845,
+ * call sites src/gpu.rs:571-790) and, as the last entry, the lm_head GEMV
+ * with select_token (src/kernels.rs:2191-2231, src/gpu.rs:800-812).  It
+ * replaces the reference's captured decode graph with programmatic edges
+ * (src/graph.rs:56-110; griddepcontrol.wait, src/kernels.rs:173-184): entry
+ * i + 1 reads its activation row only after every workgroup has finished
+ * entry i, while the weights of the entries ahead, which no entry writes,
+ * are requested before that barrier.  Outputs equal w8a8_linear /
+ * w8a8_linear_residual / w8a8_linear_argmax of each entry bit for bit.
+ *
+ * Contract: the activation rows (q, asc), weights, scales and residuals are
+ * inputs of the call -- nothing in the call writes them -- and the outputs
+ * are visible when the call completes (stream order).  The launch holds one
+ * workgroup on every CU until it ends, so sequence calls on one GPU must be
+ * stream-ordered with each other and with other work that needs CUs
+ * meanwhile; the call is not graph-capturable (W8A8_EARG under capture).
+ * Every wait inside the launch is bounded by wait_us (0: 100 ms): a wait
+ * that runs out marks the device's sequence state aborted, the launch ends,
+ * and later sequence launches return at once until
+ * w8a8_linear_sequence_reset.  w8a8_linear_sequence_status reads that
+ * state (0 = ok, 1 = a wait ran out). */
+typedef struct w8a8_seq_entry {
+  const int8_t *w;        /* [n, k], 16-byte aligned */
+  const float *ws;        /* [n] */
+  const int8_t *q;        /* [k] activation codes, 16-byte aligned */
+  const float *asc;       /* [1] activation scale */
+  void *out;              /* [n] in out_dtype; NULL only for a selecting entry */
+  const float *residual;  /* [n] f32, or NULL (then combined is NULL) */
+  void *combined;         /* [n] bf16(residual + out) in out_dtype */
+  size_t n;               /* 1 .. 64 * 15 * CUs */
+  uint32_t k;             /* 4096, 8192 or 12288 */
+  int out_dtype;          /* W8A8_OUT_F32 or W8A8_OUT_BF16 */
+  int flags;              /* W8A8_SEQ_SELECT on the last entry: greedy token */
+} w8a8_seq_entry;
+#define W8A8_SEQ_SELECT 1
+/* Bytes of the device table for count entries (64 per entry). */
+size_t w8a8_linear_sequence_table_bytes(size_t count);
+/* Validate entries[0 .. count) on the host and write their device table
+ * (16-byte aligned device memory of table_bytes) with a synchronous copy.
+ * The first call on a device also allocates its 4 KiB sequence control
+ * block (uncached device memory, held until the process ends). */
+int w8a8_linear_sequence_prepare(const w8a8_seq_entry *entries, size_t count,
+                                 void *table, size_t table_bytes);
+/* Selection keys a selecting sequence needs: 8 bytes per CU. */
+size_t w8a8_linear_sequence_workspace_bytes(void);
+/* Run a prepared table (same count).  token and workspace (8-byte aligned,
+ * w8a8_linear_sequence_workspace_bytes) are used when the last entry
+ * selects; pass NULL otherwise. */
+int w8a8_linear_sequence(void *stream, const void *table, size_t count,
+                         uint32_t *token, void *workspace,
+                         size_t workspace_bytes, uint32_t wait_us);
+/* The current device's sequence state; synchronises the device first. */
+int w8a8_linear_sequence_status(uint32_t *status);
+/* Clear an aborted state; synchronises the device first. */
+int w8a8_linear_sequence_reset(void);
+
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc): w8a8_linear_argmax with its selection keys in a fixed device

@@ -15,6 +15,15 @@ ENULL, ESHAPE, EALIGN, EINIT, EWORKSPACE, EARG, ENODEV = -1, -2, -3, -4, -5, -6,
 OUT_F32, OUT_BF16, OUT_I32 = 0, 1, 2
 PATH_AUTO, PATH_DOT4, PATH_MFMA = 0, 1, 2
 NOALLOC_MAX_ROWS = 262144  # W8A8_NOALLOC_MAX_ROWS
+SEQ_SELECT = 1  # W8A8_SEQ_SELECT
+
+
+class SeqEntry(ctypes.Structure):
+    """w8a8_seq_entry (include/inferrous_w8a8.h)."""
+    _fields_ = [("w", ctypes.c_void_p), ("ws", ctypes.c_void_p), ("q", ctypes.c_void_p),
+                ("asc", ctypes.c_void_p), ("out", ctypes.c_void_p), ("residual", ctypes.c_void_p),
+                ("combined", ctypes.c_void_p), ("n", ctypes.c_size_t), ("k", ctypes.c_uint32),
+                ("out_dtype", ctypes.c_int), ("flags", ctypes.c_int)]
 
 P = ctypes.c_void_p
 S = ctypes.c_size_t
@@ -80,6 +89,12 @@ SIGNATURES: dict[str, tuple] = {
     "w8a8_linear_argmax_workspace_bytes": (S, [S]),
     "w8a8_linear_argmax": (I, [P, P, P, P, P, S, U32, P, P, I, P, S]),
     "w8a8_linear_argmax_noalloc": (I, [P, P, P, P, P, S, U32, P, P, I]),
+    "w8a8_linear_sequence_table_bytes": (S, [S]),
+    "w8a8_linear_sequence_prepare": (I, [P, S, P, S]),
+    "w8a8_linear_sequence_workspace_bytes": (S, []),
+    "w8a8_linear_sequence": (I, [P, P, S, P, P, S, U32]),
+    "w8a8_linear_sequence_status": (I, [P]),
+    "w8a8_linear_sequence_reset": (I, []),
     "w8a8_synth_i8": (I, [P, P, S, U64, U64]),
     "w8a8_synth_f32": (I, [P, P, S, U64, U64, F, F]),
 }

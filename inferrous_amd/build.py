@@ -21,7 +21,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libinferrous_w8a8.so"
-SOURCES = ["abi.hip", "quantize.hip", "gemv.hip", "gemm.hip", "head.hip", "synth.hip"]
+SOURCES = ["abi.hip", "quantize.hip", "gemv.hip", "gemm.hip", "head.hip", "synth.hip", "sequence.hip"]
 ARCH = "gfx950"
 
 

@@ -12,6 +12,7 @@
 #include <atomic>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "../../include/inferrous_w8a8.h"
 #include "../../include/inferrous_w8a8_diag.h"
@@ -959,6 +960,187 @@ int w8a8_synth_f32(void* stream, float* out, size_t n, uint64_t seed, uint64_t s
   if (!(lo <= hi)) return W8A8_EARG;
   if (!ready()) return W8A8_EINIT;
   return hip_status(launch_synth_f32((hipStream_t)stream, out, n, seed, stream_id, lo, hi));
+}
+
+
+// ------------------------------------------------------------ decode sequence
+namespace {
+
+struct SeqDevice {
+  uint32_t* ctl = nullptr;  // uncached control block (never freed)
+  uint32_t base = 0;        // entries every workgroup announced in earlier calls
+  uint32_t grid = 0;
+};
+struct SeqTableInfo {
+  size_t count;
+  int device;
+  bool select;
+};
+std::mutex g_seq_mu;
+SeqDevice g_seq[64];
+std::vector<std::pair<const void*, SeqTableInfo>> g_seq_tables;  // prepared tables
+
+constexpr uint64_t kSeqDefaultWaitUs = 100000;
+constexpr size_t kSeqStatusIndex = kSeqGroups * 64;  // u32 index of the status word
+constexpr size_t kSeqMaxCount = 1u << 20;
+
+int current_device(int* dev) {
+  const hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return hip_status(e);
+  return *dev >= 0 && *dev < 64 ? W8A8_OK : W8A8_ENODEV;
+}
+
+// The device's control block, allocated (uncached, zeroed) on first use.
+// Caller holds g_seq_mu.
+int seq_device(int dev, SeqDevice** out) {
+  SeqDevice& d = g_seq[dev];
+  if (!d.ctl) {
+    const uint32_t grid = seq_grid();
+    if (grid == 0) return W8A8_ENODEV;
+    void* p = nullptr;
+    hipError_t e = hipExtMallocWithFlags(&p, kSeqCtlBytes, hipDeviceMallocUncached);
+    if (e != hipSuccess) return hip_status(e);
+    e = hipMemset(p, 0, kSeqCtlBytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_status(e);  // the block stays allocated: uncached memory is never freed
+    d.ctl = (uint32_t*)p;
+    d.grid = grid;
+    d.base = 0;
+  }
+  *out = &d;
+  return W8A8_OK;
+}
+
+}  // namespace
+
+size_t w8a8_linear_sequence_table_bytes(size_t count) { return count * sizeof(SeqEntry); }
+
+size_t w8a8_linear_sequence_workspace_bytes(void) {
+  if (!ready()) return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return (size_t)cus * sizeof(uint64_t);
+}
+
+int w8a8_linear_sequence_prepare(const w8a8_seq_entry* entries, size_t count, void* table, size_t table_bytes) {
+  if (!entries || !table) return W8A8_ENULL;
+  if (count == 0 || count > kSeqMaxCount) return W8A8_ESHAPE;
+  if (table_bytes < w8a8_linear_sequence_table_bytes(count)) return W8A8_EWORKSPACE;
+  if (!al(table, 16)) return W8A8_EALIGN;
+  // host-side checks of every entry first
+  for (size_t i = 0; i < count; ++i) {
+    const w8a8_seq_entry& e = entries[i];
+    if (e.flags & ~W8A8_SEQ_SELECT) return W8A8_EARG;
+    const bool select = e.flags & W8A8_SEQ_SELECT;
+    if (select && i + 1 != count) return W8A8_EARG;  // only the last entry selects
+    if (e.out_dtype != W8A8_OUT_F32 && e.out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+    if (e.k != 4096 && e.k != 8192 && e.k != 12288) return W8A8_ESHAPE;
+    if (e.n == 0 || e.n > kU32Max) return W8A8_ESHAPE;
+    if (!e.w || !e.ws || !e.q || !e.asc) return W8A8_ENULL;
+    if (!e.out && !select) return W8A8_ENULL;
+    if ((e.residual == nullptr) != (e.combined == nullptr)) return W8A8_ENULL;
+    if (select && e.residual) return W8A8_EARG;
+    if (!al(e.w, 16) || !al(e.q, 16) || !al(e.ws, 4) || !al(e.asc, 4) || !al(e.out, out_align(e.out_dtype)) ||
+        !al(e.residual, 4) || !al(e.combined, out_align(e.out_dtype)))
+      return W8A8_EALIGN;
+  }
+  if (!ready()) return W8A8_EINIT;
+  int dev = 0;
+  int st = current_device(&dev);
+  if (st != W8A8_OK) return st;
+  std::lock_guard<std::mutex> lk(g_seq_mu);
+  SeqDevice* d = nullptr;
+  st = seq_device(dev, &d);
+  if (st != W8A8_OK) return st;
+  std::vector<SeqEntry> host(count);
+  for (size_t i = 0; i < count; ++i) {
+    const w8a8_seq_entry& e = entries[i];
+    if (e.n > seq_max_rows(d->grid)) return W8A8_ESHAPE;  // 64 rows per wave at most
+    SeqEntry& t = host[i];
+    t.w = e.w;
+    t.ws = e.ws;
+    t.q = e.q;
+    t.asc = e.asc;
+    t.out = e.out;
+    t.residual = e.residual;
+    t.combined = e.combined;
+    t.n = (uint32_t)e.n;
+    t.meta = (e.k / 4096) | (e.out_dtype == W8A8_OUT_BF16 ? 4u : 0u) | (e.residual ? 8u : 0u) |
+             ((e.flags & W8A8_SEQ_SELECT) ? 16u : 0u);
+  }
+  const hipError_t e = hipMemcpy(table, host.data(), count * sizeof(SeqEntry), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_status(e);
+  const SeqTableInfo info{count, dev, (entries[count - 1].flags & W8A8_SEQ_SELECT) != 0};
+  for (auto& t : g_seq_tables)
+    if (t.first == table) {
+      t.second = info;
+      return W8A8_OK;
+    }
+  g_seq_tables.emplace_back(table, info);
+  return W8A8_OK;
+}
+
+int w8a8_linear_sequence(void* stream, const void* table, size_t count, uint32_t* token, void* workspace,
+                         size_t workspace_bytes, uint32_t wait_us) {
+  if (!table) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  int dev = 0;
+  int st = current_device(&dev);
+  if (st != W8A8_OK) return st;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing((hipStream_t)stream, &cap);
+  if (e != hipSuccess) return hip_status(e);
+  if (cap != hipStreamCaptureStatusNone) return W8A8_EARG;  // the launch argument `base` changes per call
+  std::lock_guard<std::mutex> lk(g_seq_mu);
+  const SeqTableInfo* info = nullptr;
+  for (const auto& t : g_seq_tables)
+    if (t.first == table) info = &t.second;
+  if (!info || info->count != count || info->device != dev) return W8A8_EARG;  // not prepared here
+  SeqDevice* d = nullptr;
+  st = seq_device(dev, &d);
+  if (st != W8A8_OK) return st;
+  if (info->select) {
+    if (!token || !workspace) return W8A8_ENULL;
+    if (!al(token, 4) || !al(workspace, 8)) return W8A8_EALIGN;
+    if (workspace_bytes < (size_t)d->grid * sizeof(uint64_t)) return W8A8_EWORKSPACE;
+  }
+  const uint64_t ticks = (wait_us ? (uint64_t)wait_us : kSeqDefaultWaitUs) * 100;  // 100 MHz clock
+  e = launch_sequence((hipStream_t)stream, (const SeqEntry*)table, (uint32_t)count, d->base, d->ctl,
+                      (uint64_t*)workspace, token, ticks, d->grid);
+  if (e != hipSuccess) return hip_status(e);
+  d->base += (uint32_t)count;
+  return W8A8_OK;
+}
+
+int w8a8_linear_sequence_status(uint32_t* status) {
+  if (!status) return W8A8_ENULL;
+  if (!ready()) return W8A8_EINIT;
+  int dev = 0;
+  int st = current_device(&dev);
+  if (st != W8A8_OK) return st;
+  std::lock_guard<std::mutex> lk(g_seq_mu);
+  *status = 0;
+  if (!g_seq[dev].ctl) return W8A8_OK;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(status, g_seq[dev].ctl + kSeqStatusIndex, 4, hipMemcpyDeviceToHost);
+  return hip_status(e);
+}
+
+int w8a8_linear_sequence_reset(void) {
+  if (!ready()) return W8A8_EINIT;
+  int dev = 0;
+  int st = current_device(&dev);
+  if (st != W8A8_OK) return st;
+  std::lock_guard<std::mutex> lk(g_seq_mu);
+  SeqDevice& d = g_seq[dev];
+  if (!d.ctl) return W8A8_OK;
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemset(d.ctl, 0, kSeqCtlBytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_status(e);
+  d.base = 0;
+  return W8A8_OK;
 }
 
 }  // extern "C"

@@ -147,6 +147,28 @@ size_t argmax_keys_bound(size_t n);
 
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a);
 
+// One entry of a decode-sequence table (device memory, 64 bytes).
+struct SeqEntry {
+  const int8_t* w;         // [n, k]
+  const float* ws;         // [n]
+  const int8_t* q;         // [k]
+  const float* asc;        // [1]
+  void* out;               // [n], or null (selecting entry without logits)
+  const float* residual;   // [n], with combined
+  void* combined;          // [n]
+  uint32_t n;
+  uint32_t meta;           // bits 0-1: k / 4096; bit 2: BF16 out (else F32); bit 3: residual; bit 4: selection
+};
+static_assert(sizeof(SeqEntry) == 64, "one scalar cache line pair per entry");
+constexpr int kSeqGroups = 8;              // arrival counters of the sequence barrier
+constexpr size_t kSeqCtlBytes = 4096;      // uncached control block: counters, status
+// Workgroups of a sequence launch on the current device (one per CU; 0 when
+// a CU cannot hold one), and the largest n an entry may have for that grid.
+uint32_t seq_grid();
+uint32_t seq_max_rows(uint32_t grid);
+hipError_t launch_sequence(hipStream_t st, const SeqEntry* tab, uint32_t count, uint32_t base, uint32_t* ctl,
+                           uint64_t* keys, uint32_t* token, uint64_t spin, uint32_t grid);
+
 hipError_t launch_synth_i8(hipStream_t st, int8_t* out, size_t n, uint64_t seed, uint64_t stream_id);
 hipError_t launch_synth_f32(hipStream_t st, float* out, size_t n, uint64_t seed, uint64_t stream_id,
                             float lo, float hi);

@@ -521,3 +521,84 @@ def test_workspace_queries_by_route_and_batch_range():
     assert L.w8a8_linear_workspace_bytes_upto(512, *down) == max(
         L.w8a8_linear_workspace_bytes(m, *down) for m in range(1, 513))
     assert L.w8a8_linear_workspace_bytes_upto(0, *down) == 0
+
+
+@pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")
+def test_sequence_prepare_validation_precedes_device():
+    """w8a8_linear_sequence_prepare checks every entry on the host before
+    any device call; a well-formed table stops at the init check."""
+    L = _lib.lib()
+    S = _lib.SeqEntry
+
+    def ent(**kw):
+        a = dict(w=A, ws=A, q=A, asc=A, out=A, residual=None, combined=None, n=4096, k=4096,
+                 out_dtype=_lib.OUT_BF16, flags=0)
+        a.update(kw)
+        return S(a["w"], a["ws"], a["q"], a["asc"], a["out"], a["residual"], a["combined"], a["n"], a["k"],
+                 a["out_dtype"], a["flags"])
+
+    def prep(*entries, table=A, nbytes=None, count=None):
+        arr = (S * len(entries))(*entries)
+        count = len(entries) if count is None else count
+        nbytes = 64 * len(entries) if nbytes is None else nbytes
+        return L.w8a8_linear_sequence_prepare(arr, count, table, nbytes)
+
+    assert L.w8a8_linear_sequence_table_bytes(145) == 145 * 64
+    good = ent()
+    assert prep(good, good) == _lib.EINIT
+    assert prep(good, ent(out=None, flags=_lib.SEQ_SELECT, out_dtype=_lib.OUT_F32, n=151936)) == _lib.EINIT
+    assert prep(good, ent(k=12288, residual=A, combined=A)) == _lib.EINIT
+    assert prep(good, count=0) == _lib.ESHAPE
+    assert L.w8a8_linear_sequence_prepare(None, 1, A, 64) == _lib.ENULL
+    assert prep(good, table=None) == _lib.ENULL
+    assert prep(good, good, nbytes=127) == _lib.EWORKSPACE
+    assert prep(good, table=A + 8) == _lib.EALIGN
+    assert prep(ent(k=1024)) == _lib.ESHAPE
+    assert prep(ent(k=4100)) == _lib.ESHAPE
+    assert prep(ent(n=0)) == _lib.ESHAPE
+    assert prep(ent(n=1 << 33)) == _lib.ESHAPE
+    assert prep(ent(out_dtype=_lib.OUT_I32)) == _lib.EARG
+    assert prep(ent(flags=2)) == _lib.EARG
+    assert prep(ent(flags=_lib.SEQ_SELECT), good) == _lib.EARG      # only the last entry selects
+    assert prep(ent(flags=_lib.SEQ_SELECT, residual=A, combined=A)) == _lib.EARG
+    assert prep(ent(out=None)) == _lib.ENULL
+    assert prep(ent(w=None)) == _lib.ENULL and prep(ent(q=None)) == _lib.ENULL
+    assert prep(ent(residual=A)) == _lib.ENULL and prep(ent(combined=A)) == _lib.ENULL
+    assert prep(ent(w=A + 4)) == _lib.EALIGN and prep(ent(q=A + 8)) == _lib.EALIGN
+    assert prep(ent(out=A + 1)) == _lib.EALIGN and prep(ent(ws=A + 2)) == _lib.EALIGN
+    assert prep(ent(out=A + 2, out_dtype=_lib.OUT_F32)) == _lib.EALIGN
+    assert L.w8a8_linear_sequence(None, None, 1, None, None, 0, 0) == _lib.ENULL
+    assert L.w8a8_linear_sequence(None, A, 1, None, None, 0, 0) == _lib.EINIT
+    assert L.w8a8_linear_sequence_status(None) == _lib.ENULL
+    st = ctypes.c_uint32()
+    assert L.w8a8_linear_sequence_status(ctypes.byref(st)) == _lib.EINIT
+    assert L.w8a8_linear_sequence_reset() == _lib.EINIT
+    assert L.w8a8_linear_sequence_workspace_bytes() == 0
+
+
+def test_module_sequence_checks_entries():
+    """The Python mirror refuses malformed sequence entries with
+    ValueError / TypeError before the library is called."""
+    import numpy as np
+
+    from inferrous_amd import LoadedModule
+    mod = LoadedModule(None)
+    k, n = 4096, 64
+    e = dict(q=_fake(k, np.int8), asc=_fake(1, np.float32), w=_fake(n * k, np.int8), ws=_fake(n, np.float32),
+             out=_fake(n, np.uint16))
+    with pytest.raises(ValueError, match="at least one"):
+        mod.prepare_sequence([])
+    with pytest.raises(ValueError, match="w has"):
+        mod.prepare_sequence([dict(e, w=_fake(n * k - 1, np.int8))])
+    with pytest.raises(ValueError, match="one activation row"):
+        mod.prepare_sequence([dict(e, asc=_fake(2, np.float32))])
+    with pytest.raises(ValueError, match="only the last"):
+        mod.prepare_sequence([dict(e, select=True), e])
+    with pytest.raises(ValueError, match="out is required"):
+        mod.prepare_sequence([dict(e, out=None)])
+    with pytest.raises(TypeError, match="float32 or uint16"):
+        mod.prepare_sequence([dict(e, out=_fake(n, np.int32))])
+    with pytest.raises(ValueError, match="go together"):
+        mod.prepare_sequence([dict(e, residual=_fake(n, np.float32))])
+    with pytest.raises(ValueError, match="N values"):
+        mod.prepare_sequence([dict(e, residual=_fake(n, np.float32), combined=_fake(n, np.float32))])
