@@ -48,6 +48,26 @@ __device__ __forceinline__ int8_t quant_code(float v, float s, float r) {
   return round_i8(v / s);
 }
 
+// quant_code of N values with one branch per thread: the fast product for
+// every value and, when any of them lies within quant_code's margin of a
+// rounding boundary (or is NaN), the division for all of them -- the same
+// integers as quant_code value by value.
+template <int N>
+__device__ __forceinline__ void quant_codes(const float (&v)[N], float s, float r, int (&code)[N]) {
+  bool slow = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float y = v[i] * r;
+    const float ry = __builtin_rintf(y);
+    slow |= !(__builtin_fabsf(y - ry) < 0.5f - 0x1p-12f);
+    code[i] = (int)__builtin_amdgcn_fmed3f(ry, -127.0f, 127.0f);
+  }
+  if (slow) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) code[i] = round_i8(v[i] / s);
+  }
+}
+
 // |x| as ordered bits with NaN mapped to 0 (f32::max ignores NaN,
 // src/kernels.rs:133-139); non-negative floats order like unsigned ints.
 __device__ __forceinline__ uint32_t abs_bits_no_nan(float x) {
@@ -115,18 +135,25 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max(max(a, b), max(c, d));
 }
 
-// Maximum over a 256-thread workgroup (every thread active): the wave maxima,
-// then one LDS round through red[4].  The quantizers' row maximum.
-__device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
+// Maximum over 256 threads (four whole waves, every thread active): the wave
+// maxima, then one LDS round through red[4].  The quantizers' row maximum.
+// t is the thread's index among the 256; sync() makes the four waves' LDS
+// writes visible to all of them (a workgroup barrier when they are the whole
+// workgroup).
+template <class Sync>
+__device__ __forceinline__ uint32_t block_max_256_with(uint32_t m, uint32_t* red, int t, Sync sync) {
   m = wave_max_u32(m);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
+  if ((t & 63) == 0) red[t >> 6] = m;
+  sync();
   return max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
-// RMSNorm scale of one 4096-wide row over a 256-thread workgroup, thread t
-// holding v[i] = x[t + 256 i] (i < 16).  The sum of squares keeps the
+__device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
+  return block_max_256_with(m, red, (int)threadIdx.x, [] { __syncthreads(); });
+}
+
+// RMSNorm scale of one 4096-wide row over 256 threads (four whole waves),
+// thread t holding v[i] = x[t + 256 i] (i < 16).  The sum of squares keeps the
 // reference's order exactly (src/kernels.rs:509-538, the tree of `norm`
 // :354-392): thread t sums RN(x^2) over its coordinates (sequential RN
 // adds), then the halving tree p[t] = RN(p[t] + p[t + d]), d = 128, 64, ...,
@@ -137,14 +164,16 @@ __device__ __forceinline__ uint32_t block_max_256(uint32_t m, uint32_t* red) {
 // level are unused).  inv = 1 / sqrt(mean + 1e-6) is evaluated in binary64
 // and rounded once to binary32; the reference uses an approximate rsqrt
 // (src/kernels.rs:5-6), so normalised values match it within its tolerance.
-// Returns inv to every thread, after the barrier that publishes it.
-__device__ __forceinline__ float norm_inv_4096(const float (&v)[16], float* part, float* inv) {
-  const int t = threadIdx.x;
+// Returns inv to every thread, after the sync that publishes it.  t and
+// sync as for block_max_256_with.
+template <class Sync>
+__device__ __forceinline__ float norm_inv_4096_with(const float (&v)[16], float* part, float* inv, int t,
+                                                    Sync sync) {
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) s = s + v[i] * v[i];
   part[t] = s;
-  __syncthreads();
+  sync();
   if (t < 64) {
     float a = part[t] + part[t + 128];           // d = 128 (t < 64)
     const float b = part[t + 64] + part[t + 192];  // d = 128 (t + 64 < 128)
@@ -161,8 +190,12 @@ __device__ __forceinline__ float norm_inv_4096(const float (&v)[16], float* part
       *inv = (float)(1.0 / __builtin_sqrt((double)m));
     }
   }
-  __syncthreads();
+  sync();
   return *inv;
+}
+
+__device__ __forceinline__ float norm_inv_4096(const float (&v)[16], float* part, float* inv) {
+  return norm_inv_4096_with(v, part, inv, (int)threadIdx.x, [] { __syncthreads(); });
 }
 
 // The 64-bit maximum keeps the cross-lane shuffle form.  Its users are the

@@ -331,134 +331,6 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_m1_timed(const int8_t* w
   gemv_m1_body<R, KC, EPI_PLAIN, kGemvWaves, true>(o, nullptr, nullptr, stamps);
 }
 
-// The producer of the activation codes folded into the prologue of the M = 1
-// GEMV that consumes them: norm_quantize (src/kernels.rs:476-575) or
-// quantize (src/kernels.rs:433-451) of one 4096-wide f32 row, then linear /
-// linear_residual (src/kernels.rs:577-618, :807-845) on one matrix.  Every
-// workgroup loads the row (and the gains) ahead of its weight stream and
-// recomputes the row's scale with the producer's own arithmetic and order,
-// and its codes with quant_code (the same integers as the producer's
-// division), so every workgroup holds the same bits the producer kernel
-// would have written; they reach the dot products through LDS.  Workgroup 0
-// also writes the producer's outputs (codes, scale, the normalised row when
-// asked for, the maxima reset).  One launch instead of two: measured on
-// MI355X in graphs of 36 distinct-weight pairs, norm_quantize + qkv
-// (6144 x 4096) 8.45 -> 7.43 us, quantize + o (4096 x 4096) 6.64 -> 5.30 us.
-// The SwiGLU GEMV takes the same fold with two coordinates per wave
-// (gemv_swiglu_norm, below).
-enum { PROD_QUANT = 1, PROD_NORM = 2 };
-
-struct ProducerLds {
-  float part[256];
-  float inv;
-  uint32_t red[4];
-  alignas(16) int8_t qs[4096];
-};
-
-// The producer's half of a folded kernel, over the workgroup's 256 threads,
-// thread t holding v[i] = x[t + 256 i] (and g[i] = gain[t + 256 i]): the
-// row's codes into L.qs (visible after the next barrier) and its scale,
-// returned.  v is left holding the normalised values (PROD_NORM).
-template <int PROD>
-__device__ __forceinline__ float producer_codes(float (&v)[16], const float (&g)[16], ProducerLds& L) {
-  static_assert(kGemvThreads == 256, "the producers' element order is laid out over 256 threads");
-  const int t = threadIdx.x;
-  uint32_t mb = kFloorBits;
-  if (PROD == PROD_NORM) {
-    const float inv = norm_inv_4096(v, L.part, &L.inv);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      v[i] = bf16_rne((v[i] * inv) * g[i]);
-      mb = max(mb, abs_bits_no_nan(v[i]));
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) mb = max(mb, abs_bits_no_nan(v[i]));
-  }
-  mb = block_max_256(mb, L.red);
-  const float sc = __uint_as_float(mb) / 127.0f, rc = 1.0f / sc;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) L.qs[t + 256 * i] = quant_code(v[i], sc, rc);
-  return sc;
-}
-
-// Workgroup 0 writes what the producer kernel would have written: the
-// normalised row (when asked for), the scale and the maxima reset now, the
-// codes after the barrier that publishes L.qs (producer_codes_out).
-template <int PROD>
-__device__ __forceinline__ void producer_outputs(const float (&v)[16], float sc, float* normed, float* scale_out,
-                                                 uint32_t* maxima) {
-  if (blockIdx.x != 0) return;
-  const int t = threadIdx.x;
-  if (PROD == PROD_NORM && normed)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) normed[t + 256 * i] = v[i];
-  if (t == 0) {
-    scale_out[0] = sc;
-    if (maxima) maxima[0] = kFloorBits;
-  }
-}
-
-__device__ __forceinline__ void producer_codes_out(const ProducerLds& L, int8_t* q_out) {
-  if (blockIdx.x == 0)
-    *reinterpret_cast<v4i*>(q_out + threadIdx.x * 16) = *reinterpret_cast<const v4i*>(L.qs + threadIdx.x * 16);
-}
-
-template <int R, int EPI, int PROD>
-__global__ __launch_bounds__(kGemvThreads) void gemv_m1_produce(
-    const float* x, const float* gain, const int8_t* w, const float* ws, uint32_t n, int dtype,
-    const float* residual, void* out, void* combined, int8_t* q_out, float* scale_out, uint32_t* maxima,
-    float* normed) {
-  __shared__ ProducerLds L;
-  const int t = threadIdx.x, lane = t & 63;
-  const uint32_t row0 = (blockIdx.x * kGemvWaves + wave_id()) * R;
-  // The producer's operands are loaded first: loads complete in issue order,
-  // so its math then waits for them alone while the weights are in flight.
-  float v[16], g[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    v[i] = x[t + 256 * i];
-    g[i] = PROD == PROD_NORM ? gain[t + 256 * i] : 0.f;
-  }
-  // The epilogue's operands and the weight stream; tail rows recompute the
-  // last row (n >= 1).
-  const uint32_t erow = min(row0 + (uint32_t)min(lane, R - 1), n - 1);
-  const float wsc = ws[erow];
-  const float resid = EPI == EPI_RESIDUAL ? residual[erow] : 0.f;
-  v4i wv[R][4];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int8_t* p = w + (size_t)min(row0 + r, n - 1) * 4096 + lane * 16;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) wv[r][c] = load_nt16(p + c * 1024);
-  }
-  const float sc = producer_codes<PROD>(v, g, L);
-  producer_outputs<PROD>(v, sc, normed, scale_out, maxima);
-  __syncthreads();
-  v4i xq[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) xq[c] = *reinterpret_cast<const v4i*>(L.qs + c * 1024 + lane * 16);
-  producer_codes_out(L, q_out);
-  int acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    acc[r] = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[r] = dot16(xq[c], wv[r][c], acc[r]);
-  }
-  const int total = reduce_to_lanes<R>(acc, lane);
-  const uint32_t row = row0 + lane;
-  const bool writer = lane < R && row < n;
-  // computed on every lane and pinned, as in gemv_m1_body
-  const float value = dequant(total, sc, wsc);
-  const float comb = EPI == EPI_RESIDUAL ? bf16_rne(resid + value) : 0.f;
-  asm volatile("" ::"v"(value), "v"(comb), "s"(dtype));
-  if (writer) {
-    if (out) store_out(out, row, dtype, total, value);
-    if (EPI == EPI_RESIDUAL) store_out(combined, row, dtype, total, comb);
-  }
-}
-
 // Any m (blockIdx.y selects MT activation rows), any k % 16 == 0.
 template <int R, int MT, int U, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void gemv_mt(GemvArgs a) {
@@ -605,73 +477,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_swiglu(SwigluArgs a) {
   }
 }
 
-// norm_quantize folded into the M = 1 SwiGLU GEMV (K = 4096), as
-// gemv_m1_produce folds it into linear: every workgroup recomputes the row's
-// codes.  Each wave owns RC consecutive coordinates (their gate and up rows):
-// with one coordinate per wave the 3,072 workgroups' repeated norm did not
-// hide behind the weight stream (norm_quantize + SwiGLU GEMV 19.8 us as two
-// launches, 20.0-20.3 as one); with two, 18.7 us.  The plain GEMV keeps one
-// coordinate per wave (16.5 against 17.3 us with two).
-template <int RC>
-__global__ __launch_bounds__(kGemvThreads) void gemv_swiglu_norm(
-    const float* x, const float* gain, const int8_t* wg, const float* wsg, const int8_t* wu, const float* wsu,
-    uint32_t n, int dtype, void* gate, void* up, void* act, int8_t* q_out, float* scale_out, uint32_t* maxima,
-    float* normed) {
-  __shared__ ProducerLds L;
-  const int t = threadIdx.x, lane = t & 63;
-  const uint32_t c0 = (blockIdx.x * kGemvWaves + wave_id()) * RC;
-  float v[16], g[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    v[i] = x[t + 256 * i];
-    g[i] = gain[t + 256 * i];
-  }
-  // epilogue operands and weights; tail coordinates recompute the last (n >= 1)
-  float sg[RC], su[RC];
-  v4i wgv[RC][4], wuv[RC][4];
-#pragma unroll
-  for (int rc = 0; rc < RC; ++rc) {
-    const uint32_t cr = min(c0 + rc, n - 1);
-    sg[rc] = wsg[cr];
-    su[rc] = wsu[cr];
-    const int8_t* pg = wg + (size_t)cr * 4096 + lane * 16;
-    const int8_t* pu = wu + (size_t)cr * 4096 + lane * 16;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      wgv[rc][i] = load_nt16(pg + i * 1024);
-      wuv[rc][i] = load_nt16(pu + i * 1024);
-    }
-  }
-  const float sc = producer_codes<PROD_NORM>(v, g, L);
-  producer_outputs<PROD_NORM>(v, sc, normed, scale_out, maxima);
-  __syncthreads();
-  v4i xq[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) xq[i] = *reinterpret_cast<const v4i*>(L.qs + i * 1024 + lane * 16);
-  producer_codes_out(L, q_out);
-#pragma unroll
-  for (int rc = 0; rc < RC; ++rc) {
-    int ag = 0, au = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ag = dot16(xq[i], wgv[rc][i], ag);
-      au = dot16(xq[i], wuv[rc][i], au);
-    }
-    const int tg = wave_sum_uniform(ag);
-    const int tu = wave_sum_uniform(au);
-    const float gv = dequant(tg, sc, sg[rc]);
-    const float uv = dequant(tu, sc, su[rc]);
-    const float av = silu_mul(gv, uv);
-    asm volatile("" ::"v"(av), "s"(dtype));
-    const uint32_t c = c0 + rc;
-    if (c < n && lane == 0) {
-      store_out(gate, c, dtype, tg, gv);
-      store_out(up, c, dtype, tu, uv);
-      store_out(act, c, dtype, 0, av);
-    }
-  }
-}
-
 __device__ __forceinline__ float load_val(const void* p, size_t i, int dtype) {
   if (dtype == W8A8_OUT_BF16)
     return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
@@ -747,88 +552,416 @@ __global__ __launch_bounds__(kRowTailThreads) void swiglu_row_tail(const void* a
   }
 }
 
-// The SwiGLU row tail folded into the M = 1 down GEMV that consumes its
-// codes (gemv_m1_rowtail): swiglu_row_tail<true>'s work -- the act row's
-// largest bits(|act|) (NaN -> 0) folded into maxima[0], then
-// quantize_with_max (src/kernels.rs:453-475) with that maximum, s =
-// RN(from_bits(max(m0, row max)) / 127), q_j = round(RN(act_j / s)) -- then
-// linear / linear_residual (src/kernels.rs:577-618) on one matrix of
-// K = 12,288.  Every workgroup loads the act row ahead of its weights,
-// reduces the row maximum with the row tail's expressions and quantizes the
-// row to the row tail's codes (quant_code: the same integers without a
-// division per element), so it holds the codes and scale the row tail would
-// have written; they reach the dot products through LDS.  m0 is maxima[0] as a
-// workgroup reads it: the call's value, or that value with the row maximum
-// folded in by workgroup 0's atomicMax -- max(m0, row max) is the same
-// either way.  Workgroup 0 also writes the codes and the scale (when asked
-// for) and folds the maximum, so the state after the call is the row
-// tail's.  Sixteen waves per workgroup, one row each: every workgroup
-// repeats the row's 12,288 divisions, so fewer, larger workgroups pay less
-// for them.  Measured on MI355X, graphs of 36 distinct-weight launches,
-// row tail + down with residual: 14.46 us per layer as two launches, 11.88
-// folded with 16 waves, 13.05 with 8, 16.85 with 4.
-constexpr int kRowtailWaves = 16;
-constexpr uint32_t kRowtailWidth = 12288;
+// ------------------------------------------------ folded producers, split roles
+// The producer of a GEMV's activation codes folded into the GEMV launch:
+// norm_quantize (src/kernels.rs:476-575) or quantize (:433-451) of one
+// 4096-wide f32 row before linear / linear_residual (src/kernels.rs:577-618,
+// :807-845) or linear_swiglu (:619-695), and the SwiGLU row tail
+// (quantize_with_max with the act row's maximum folded in, :453-475 and
+// :133-147) before the down projection of K = 12,288.  Every workgroup
+// derives the codes itself, with the producer kernel's arithmetic and
+// order, so it holds the bits the producer would have written; workgroup 0
+// also writes the producer's outputs.  One launch instead of two.
+//
+// Roles.  A CU holds back the issue of further vector-memory loads while
+// many of its requests are in flight: measured on MI355X with per-wave clock
+// stamps, of sixteen waves that each stream a 12 KiB row, the k-th wave on
+// each SIMD finished issuing its loads about k x 1.7 us after the launch.  A
+// producer whose waves also stream weights, meeting at workgroup barriers,
+// therefore waits for the last wave to issue its weights -- near the end of
+// the stream -- before its codes exist (2-3 us of the 9-19 us launches).  So
+// the roles are split: four producer waves load the row, and a barrier
+// orders those loads ahead of every weight load of the workgroup; the NS
+// streaming waves then issue their weights and meet the producers once
+// more, at the hand-off barrier, which publishes the codes and the scale.
+// The producers meet among themselves through an LDS counter (prod_sync),
+// never at a workgroup barrier, so the streamers' held-back issue does not
+// delay them.  One workgroup per CU at the decode shapes.
+enum { PROD_QUANT = 1, PROD_NORM = 2 };
+constexpr int kProdWaves = 4;
+// KiB of its first row each streaming wave requests before the first
+// barrier.  Measured on MI355X: two KiB delayed the barrier (the producer's
+// row loads then queue behind them) and gained nothing, so none.
+constexpr int kSplitLead = 0;
 
-template <int EPI>
-__global__ __launch_bounds__(kRowtailWaves * kWave) void gemv_m1_rowtail(
-    const void* act, int act_dtype, uint32_t* maxima, const int8_t* w, const float* ws, uint32_t n, int dtype,
-    const float* residual, void* out, void* combined, int8_t* q_out, float* scale_out) {
-  constexpr int T = kRowtailWaves * kWave, PER = kRowtailWidth / T, KC = kRowtailWidth / 1024;
-  static_assert(kRowtailWidth % T == 0, "the row splits evenly over the workgroup");
-  __shared__ __attribute__((aligned(16))) int8_t qs[kRowtailWidth];
-  __shared__ uint32_t wmax[kRowtailWaves];
-  const int t = threadIdx.x, lane = t & 63, wv = wave_id();
-  // The producer's operands first: loads complete in issue order, so its
-  // math waits for them alone while the weights are in flight.
-  float v[PER];
+template <int K>
+struct SplitLds {
+  float part[256];
+  float inv;
+  uint32_t red[4];
+  uint32_t count;  // producer-wave arrivals (prod_sync)
+  float scale;
+  alignas(16) int8_t qs[K];
+};
+
+// The row slot of workgroup b among G.  The dispatcher deals workgroups to
+// the eight XCDs in turn (b on XCD b mod 8); slot (b mod 8) (G / 8) + b / 8
+// gives each XCD a contiguous range of slots, so that at each step an XCD's
+// streaming waves read consecutive rows, spread over the HBM channels,
+// instead of every eighth row.  Measured on MI355X with per-workgroup clock
+// stamps: with slot = b, one XCD's workgroups ended up to 2 us after
+// another's in the 12,288-coordinate SwiGLU GEMV.
+__device__ __forceinline__ uint32_t xcd_slot(uint32_t b, uint32_t G) {
+  return G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
+}
+
+// Workgroup barrier that orders the LDS operations before it and nothing
+// else: a wave's outstanding global loads stay in flight across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The producer waves' own barrier: each adds one to *count and waits until
+// the count reaches the next multiple of kProdWaves.  Every producer wave
+// arrives (none of them waits on anything but its own row loads), so the
+// waits end; the other waves never touch the counter.
+__device__ __forceinline__ void prod_sync(uint32_t* count, uint32_t& target) {
+  target += kProdWaves;
+  __builtin_amdgcn_wave_barrier();
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+    __builtin_amdgcn_s_sleep(1);
+}
+
+// The K = 4096 producer, run by the producer waves (pt = 0..255) holding
+// v[i] = x[pt + 256 i] and g[i] = gain[pt + 256 i]: the codes into L.qs and
+// the scale into L.scale, with norm_quantize's / quantize's arithmetic
+// (norm_inv_4096's order, the same maximum, quant_code's integers).
+// Workgroup 0 also writes the normalised row (when asked for), the scale
+// and the maxima reset.
+template <int PROD>
+__device__ __forceinline__ void split_producer_4096(float (&v)[16], const float (&g)[16], SplitLds<4096>& L,
+                                                    int pt, float* normed, float* scale_out,
+                                                    uint32_t* maxima) {
+  uint32_t target = 0;
+  auto sync = [&] { prod_sync(&L.count, target); };
+  uint32_t mb = kFloorBits;
+  if (PROD == PROD_NORM) {
+    const float inv = norm_inv_4096_with(v, L.part, &L.inv, pt, sync);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) v[i] = load_val(act, t + (size_t)T * i, act_dtype);
-  const uint32_t m0 = maxima[0];
-  const uint32_t row0 = blockIdx.x * kRowtailWaves + wv;
-  const uint32_t erow = min(row0, n - 1);  // tail rows recompute the last row (n >= 1)
-  const float wsc = ws[erow];
-  const float resid = EPI == EPI_RESIDUAL ? residual[erow] : 0.f;
-  v4i wt[KC];
-  const int8_t* p = w + (size_t)erow * kRowtailWidth + lane * 16;
+    for (int i = 0; i < 16; ++i) {
+      v[i] = bf16_rne((v[i] * inv) * g[i]);
+      mb = max(mb, abs_bits_no_nan(v[i]));
+    }
+  } else {
 #pragma unroll
-  for (int c = 0; c < KC; ++c) wt[c] = load_nt16(p + c * 1024);
-  uint32_t bits = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) bits = max(bits, abs_bits_no_nan(v[i]));
-  bits = wave_max_u32(bits);
-  if (lane == 0) wmax[wv] = bits;
-  __syncthreads();
-  uint32_t rmax = 0;
-#pragma unroll
-  for (int j = 0; j < kRowtailWaves; ++j) rmax = max(rmax, wmax[j]);
-  const float sc = __uint_as_float(max(m0, rmax)) / 127.0f, rc = 1.0f / sc;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) qs[t + T * i] = quant_code(v[i], sc, rc);
-  if (blockIdx.x == 0 && t == 0) {
-    atomicMax(maxima, rmax);
-    if (scale_out) scale_out[0] = sc;
+    for (int i = 0; i < 16; ++i) mb = max(mb, abs_bits_no_nan(v[i]));
   }
-  __syncthreads();
-  if (blockIdx.x == 0 && q_out && t < (int)(kRowtailWidth / 16))
-    *reinterpret_cast<v4i*>(q_out + t * 16) = *reinterpret_cast<const v4i*>(qs + t * 16);
-  v4i xq[KC];
+  mb = block_max_256_with(mb, L.red, pt, sync);
+  const float sc = __uint_as_float(mb) / 127.0f, rc = 1.0f / sc;
+  int code[16];
+  quant_codes(v, sc, rc, code);
 #pragma unroll
-  for (int c = 0; c < KC; ++c) xq[c] = *reinterpret_cast<const v4i*>(qs + c * 1024 + lane * 16);
-  int acc[1] = {0};
+  for (int i = 0; i < 16; ++i) L.qs[pt + 256 * i] = (int8_t)code[i];
+  if (pt == 0) L.scale = sc;
+  if (blockIdx.x != 0) return;
+  if (PROD == PROD_NORM && normed)
 #pragma unroll
-  for (int c = 0; c < KC; ++c) acc[0] = dot16(xq[c], wt[c], acc[0]);
-  const int total = reduce_to_lanes<1>(acc, lane);
-  const bool writer = lane == 0 && row0 < n;
-  // computed on every lane and pinned, as in gemv_m1_body
-  const float value = dequant(total, sc, wsc);
-  const float comb = EPI == EPI_RESIDUAL ? bf16_rne(resid + value) : 0.f;
-  asm volatile("" ::"v"(value), "v"(comb), "s"(dtype));
-  if (writer) {
-    if (out) store_out(out, row0, dtype, total, value);
-    if (EPI == EPI_RESIDUAL) store_out(combined, row0, dtype, total, comb);
+    for (int i = 0; i < 16; ++i) normed[pt + 256 * i] = v[i];
+  if (pt == 0) {
+    scale_out[0] = sc;
+    if (maxima) maxima[0] = kFloorBits;
   }
 }
+
+// The producer waves' row loads (thread pt of the four).
+template <int PROD>
+__device__ __forceinline__ void split_load_4096(const float* x, const float* gain, int pt, float (&v)[16],
+                                                float (&g)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    v[i] = x[pt + 256 * i];
+    g[i] = PROD == PROD_NORM ? gain[pt + 256 * i] : 0.f;
+  }
+}
+
+// Workgroup 0's producer waves copy the codes out after the hand-off.
+template <int K>
+__device__ __forceinline__ void split_codes_out(const SplitLds<K>& L, int pt, int8_t* q_out) {
+  if (blockIdx.x != 0 || !q_out) return;
+  for (int i = pt; i < K / 16; i += kProdWaves * kWave)
+    *reinterpret_cast<v4i*>(q_out + i * 16) = *reinterpret_cast<const v4i*>(L.qs + i * 16);
+}
+
+// linear / linear_residual with the K = 4096 producer folded in: NS
+// streaming waves of RS consecutive rows each (workgroup b: rows
+// [b NS RS, (b + 1) NS RS)), four producer waves.  Tail rows recompute the
+// last row (n >= 1).
+template <int NS, int RS, int EPI, int PROD>
+__global__ __launch_bounds__((NS + kProdWaves) * kWave) void gemv_m1_split(
+    const float* x, const float* gain, const int8_t* w, const float* ws, uint32_t n, int dtype,
+    const float* residual, void* out, void* combined, int8_t* q_out, float* scale_out, uint32_t* maxima,
+    float* normed) {
+  __shared__ SplitLds<4096> L;
+  const int t = threadIdx.x, lane = t & 63;
+  const uint32_t wv = wave_id();
+  const int pt = t - NS * kWave;
+  const bool producer = wv >= NS;
+  if (t == 0) L.count = 0;
+  // row r of a streaming wave: (r NS + wave) G + workgroup, so that the
+  // streamers of all workgroups sweep one window of the matrix together
+  const uint32_t G = gridDim.x;
+  auto row_of = [&](int r) -> uint32_t { return ((uint32_t)r * NS + wv) * G + xcd_slot(blockIdx.x, G); };
+  auto wrow = [&](int r) { return w + (size_t)min(row_of(r), n - 1) * 4096 + lane * 16; };
+  float v[16], g[16];
+  v4i wt[RS][4];
+  if (producer)
+    split_load_4096<PROD>(x, gain, pt, v, g);
+  else
+#pragma unroll
+    for (int c = 0; c < kSplitLead; ++c) wt[0][c] = load_nt16(wrow(0) + c * 1024);
+  lds_barrier();  // the row loads ahead of the weight stream; L.count zeroed
+  if (producer) {
+    split_producer_4096<PROD>(v, g, L, pt, normed, scale_out, maxima);
+    lds_barrier();  // hand-off
+    split_codes_out(L, pt, q_out);
+    return;
+  }
+  float wsr[RS], rsr[RS];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const uint32_t er = min(row_of(r), n - 1);
+    wsr[r] = ws[er];
+    rsr[r] = EPI == EPI_RESIDUAL ? residual[er] : 0.f;
+#pragma unroll
+    for (int c = r == 0 ? kSplitLead : 0; c < 4; ++c) wt[r][c] = load_nt16(wrow(r) + c * 1024);
+  }
+  lds_barrier();  // hand-off: codes and scale
+  const float sc = L.scale;
+  v4i xq[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) xq[c] = *reinterpret_cast<const v4i*>(L.qs + c * 1024 + lane * 16);
+  int acc[RS];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    acc[r] = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[r] = dot16(xq[c], wt[r][c], acc[r]);
+  }
+  const int total = reduce_to_lanes<RS>(acc, lane);
+  float wl = wsr[0], rl = rsr[0];
+  uint32_t row = row_of(0);
+#pragma unroll
+  for (int r = 1; r < RS; ++r) {
+    wl = lane == r ? wsr[r] : wl;
+    rl = lane == r ? rsr[r] : rl;
+    row = lane == r ? row_of(r) : row;
+  }
+  const float value = dequant(total, sc, wl);
+  const float comb = EPI == EPI_RESIDUAL ? bf16_rne(rl + value) : 0.f;
+  asm volatile("" ::"v"(value), "v"(comb), "s"(dtype));
+  if (lane < RS && row < n) {
+    if (out) store_out(out, row, dtype, total, value);
+    if (EPI == EPI_RESIDUAL) store_out(combined, row, dtype, total, comb);
+  }
+}
+
+// linear_swiglu with norm_quantize folded in: NS streaming waves of CS
+// consecutive coordinates each (a coordinate: its gate row and its up row,
+// 8 KiB), two coordinates in flight per wave, four producer waves.  Lane 0
+// writes gate, up (bit-exact linear epilogues) and act = silu_mul(gate, up).
+template <int NS, int CS>
+__global__ __launch_bounds__((NS + kProdWaves) * kWave) void gemv_swiglu_split(
+    const float* x, const float* gain, const int8_t* wg, const float* wsg, const int8_t* wu, const float* wsu,
+    uint32_t n, int dtype, void* gate, void* up, void* act, int8_t* q_out, float* scale_out, uint32_t* maxima,
+    float* normed) {
+  static_assert(CS % 2 == 0, "coordinates go through two register slots");
+  __shared__ SplitLds<4096> L;
+  const int t = threadIdx.x, lane = t & 63;
+  const uint32_t wv = wave_id();
+  const int pt = t - NS * kWave;
+  if (t == 0) L.count = 0;
+  // coordinate k of a streaming wave: (k NS + wave) G + workgroup, so that
+  // the streamers of all workgroups sweep one window of the matrices together
+  const uint32_t G = gridDim.x;
+  auto coord = [&](int k) -> uint32_t { return ((uint32_t)k * NS + wv) * G + xcd_slot(blockIdx.x, G); };
+  auto grow = [&](int k) { return wg + (size_t)min(coord(k), n - 1) * 4096 + lane * 16; };
+  auto urow = [&](int k) { return wu + (size_t)min(coord(k), n - 1) * 4096 + lane * 16; };
+  float v[16], g[16];
+  v4i ga[4], ua[4], gb[4], ub[4];
+  if (wv >= NS)
+    split_load_4096<PROD_NORM>(x, gain, pt, v, g);
+  else
+#pragma unroll
+    for (int i = 0; i < kSplitLead; ++i) ga[i] = load_nt16(grow(0) + i * 1024);
+  lds_barrier();
+  if (wv >= NS) {
+    split_producer_4096<PROD_NORM>(v, g, L, pt, normed, scale_out, maxima);
+    lds_barrier();
+    split_codes_out(L, pt, q_out);
+    return;
+  }
+  float sg[CS], su[CS];
+#pragma unroll
+  for (int k = 0; k < CS; ++k) {
+    const uint32_t cr = min(coord(k), n - 1);
+    sg[k] = wsg[cr];
+    su[k] = wsu[cr];
+  }
+  auto issue = [&](v4i (&gv)[4], v4i (&uv)[4], int k, int from) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i >= from) gv[i] = load_nt16(grow(k) + i * 1024);
+      uv[i] = load_nt16(urow(k) + i * 1024);
+    }
+  };
+  issue(ga, ua, 0, kSplitLead);
+  issue(gb, ub, 1, 0);
+  lds_barrier();  // hand-off
+  const float sc = L.scale;
+  v4i xq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xq[i] = *reinterpret_cast<const v4i*>(L.qs + i * 1024 + lane * 16);
+  auto finish = [&](const v4i (&gv)[4], const v4i (&uv)[4], int k) {
+    int ag = 0, au = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ag = dot16(xq[i], gv[i], ag);
+      au = dot16(xq[i], uv[i], au);
+    }
+    const int tg = wave_sum_uniform(ag);
+    const int tu = wave_sum_uniform(au);
+    const float gv_ = dequant(tg, sc, sg[k]);
+    const float uv_ = dequant(tu, sc, su[k]);
+    const float av = silu_mul(gv_, uv_);
+    asm volatile("" ::"v"(av), "s"(dtype));
+    const uint32_t c = coord(k);
+    if (c < n && lane == 0) {
+      store_out(gate, c, dtype, tg, gv_);
+      store_out(up, c, dtype, tu, uv_);
+      store_out(act, c, dtype, 0, av);
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < CS; k += 2) {
+    finish(ga, ua, k);
+    if (k + 2 < CS) issue(ga, ua, k + 2, 0);
+    finish(gb, ub, k + 1);
+    if (k + 3 < CS) issue(gb, ub, k + 3, 0);
+  }
+}
+
+// The SwiGLU row tail folded into the down GEMV (K = 12,288) that consumes
+// its codes: swiglu_row_tail<true>'s work -- the act row's largest
+// bits(|act|) (NaN -> 0) folded into maxima[0], then quantize_with_max
+// (src/kernels.rs:453-475) with that maximum, s = RN(from_bits(max(m0, row
+// max)) / 127), q_j = round(RN(act_j / s)) -- then linear / linear_residual
+// on one matrix.  m0 is maxima[0] as a workgroup reads it: the call's value,
+// or that value with the row maximum folded in by workgroup 0's atomicMax
+// -- max(m0, row max) is the same either way.  Producer thread pt holds
+// elements 4 (pt + 256 j) .. + 3 (j < 12): one 16-byte (F32) or 8-byte
+// (BF16) load each.  NS streaming waves of RS rows.
+constexpr uint32_t kRowtailWidth = 12288;
+
+template <int NS, int RS, int EPI, bool BF16_ACT>
+__global__ __launch_bounds__((NS + kProdWaves) * kWave) void gemv_rowtail_split(
+    const void* act, uint32_t* maxima, const int8_t* w, const float* ws, uint32_t n, int dtype,
+    const float* residual, void* out, void* combined, int8_t* q_out, float* scale_out) {
+  constexpr int KC = kRowtailWidth / 1024, J = kRowtailWidth / (4 * kProdWaves * kWave);
+  __shared__ SplitLds<kRowtailWidth> L;
+  const int t = threadIdx.x, lane = t & 63;
+  const uint32_t wv = wave_id();
+  const int pt = t - NS * kWave;
+  if (t == 0) L.count = 0;
+  const uint32_t G = gridDim.x;
+  auto row_of = [&](int r) -> uint32_t { return ((uint32_t)r * NS + wv) * G + xcd_slot(blockIdx.x, G); };
+  auto wrow = [&](int r) { return w + (size_t)min(row_of(r), n - 1) * kRowtailWidth + lane * 16; };
+  uint32_t raw[BF16_ACT ? 2 * J : 4 * J];  // the thread's act values as loaded
+  uint32_t m0 = 0;
+  v4i wt[RS][KC];
+  if (wv < NS) {
+#pragma unroll
+    for (int c = 0; c < kSplitLead; ++c) wt[0][c] = load_nt16(wrow(0) + c * 1024);
+  } else {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (BF16_ACT) {
+        const v2i d = reinterpret_cast<const v2i*>(act)[pt + 256 * j];
+        raw[2 * j] = (uint32_t)d.x;
+        raw[2 * j + 1] = (uint32_t)d.y;
+      } else {
+        const v4i d = reinterpret_cast<const v4i*>(act)[pt + 256 * j];
+        raw[4 * j] = (uint32_t)d.x;
+        raw[4 * j + 1] = (uint32_t)d.y;
+        raw[4 * j + 2] = (uint32_t)d.z;
+        raw[4 * j + 3] = (uint32_t)d.w;
+      }
+    }
+    m0 = maxima[0];
+  }
+  lds_barrier();
+  if (wv >= NS) {
+    // element i of the thread (i < 4 J): act[4 (pt + 256 (i / 4)) + i % 4]
+    auto val = [&](int i) -> float {
+      if (!BF16_ACT) return __uint_as_float(raw[i]);
+      const uint32_t d = raw[i >> 1];
+      return __uint_as_float((i & 1) ? (d & 0xffff0000u) : (d << 16));
+    };
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < 4 * J; ++i) bits = max(bits, abs_bits_no_nan(val(i)));
+    uint32_t target = 0;
+    const uint32_t rmax = block_max_256_with(bits, L.red, pt, [&] { prod_sync(&L.count, target); });
+    const float sc = __uint_as_float(max(m0, rmax)) / 127.0f, rc = 1.0f / sc;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float e[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) e[u] = val(4 * j + u);
+      int code[4];
+      quant_codes(e, sc, rc, code);
+      reinterpret_cast<uint32_t*>(L.qs)[pt + 256 * j] = (uint32_t)(code[0] & 0xff) |
+                                                          ((uint32_t)(code[1] & 0xff) << 8) |
+                                                          ((uint32_t)(code[2] & 0xff) << 16) |
+                                                          ((uint32_t)code[3] << 24);
+    }
+    if (pt == 0) {
+      L.scale = sc;
+      if (blockIdx.x == 0) {
+        atomicMax(maxima, rmax);
+        if (scale_out) scale_out[0] = sc;
+      }
+    }
+    lds_barrier();  // hand-off
+    split_codes_out(L, pt, q_out);
+    return;
+  }
+  float wsr[RS], rsr[RS];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const uint32_t er = min(row_of(r), n - 1);
+    wsr[r] = ws[er];
+    rsr[r] = EPI == EPI_RESIDUAL ? residual[er] : 0.f;
+#pragma unroll
+    for (int c = r == 0 ? kSplitLead : 0; c < KC; ++c) wt[r][c] = load_nt16(wrow(r) + c * 1024);
+  }
+  lds_barrier();  // hand-off
+  const float sc = L.scale;
+  int acc[RS];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) acc[r] = 0;
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    const v4i xq = *reinterpret_cast<const v4i*>(L.qs + c * 1024 + lane * 16);
+#pragma unroll
+    for (int r = 0; r < RS; ++r) acc[r] = dot16(xq, wt[r][c], acc[r]);
+  }
+  const int total = reduce_to_lanes<RS>(acc, lane);
+  float wl = wsr[0], rl = rsr[0];
+  uint32_t row = row_of(0);
+#pragma unroll
+  for (int r = 1; r < RS; ++r) {
+    wl = lane == r ? wsr[r] : wl;
+    rl = lane == r ? rsr[r] : rl;
+    row = lane == r ? row_of(r) : row;
+  }
+  const float value = dequant(total, sc, wl);
+  const float comb = EPI == EPI_RESIDUAL ? bf16_rne(rl + value) : 0.f;
+  asm volatile("" ::"v"(value), "v"(comb), "s"(dtype));
+  if (lane < RS && row < n) {
+    if (out) store_out(out, row, dtype, total, value);
+    if (EPI == EPI_RESIDUAL) store_out(combined, row, dtype, total, comb);
+  }
+}
+
 
 // swiglu (src/kernels.rs:2172-2190): act = silu_mul(gate, up) elementwise
 // over rows x width (blockIdx.y = row); with maxima, each row's largest
@@ -974,24 +1107,22 @@ hipError_t launch_gemv(hipStream_t st, GemvArgs& a) {
   return dispatch<EPI_PLAIN>(st, a, &blocks);
 }
 
-template <int R, int EPI, int PROD>
-static hipError_t launch_produce(hipStream_t st, const ProduceArgs& p) {
-  const uint32_t blocks = (p.n + R * kGemvWaves - 1) / (R * kGemvWaves);
-  hipLaunchKernelGGL((gemv_m1_produce<R, EPI, PROD>), dim3(blocks), dim3(kGemvThreads), 0, st, p.x, p.gain, p.w,
-                     p.ws, p.n, p.out_dtype, p.residual, p.out, p.combined, p.q, p.scale, p.maxima, p.normed);
+template <int NS, int RS, int EPI, int PROD>
+static hipError_t launch_split(hipStream_t st, const ProduceArgs& p) {
+  const uint32_t blocks = (p.n + NS * RS - 1) / (NS * RS);
+  hipLaunchKernelGGL((gemv_m1_split<NS, RS, EPI, PROD>), dim3(blocks), dim3((NS + kProdWaves) * kWave), 0, st, p.x,
+                     p.gain, p.w, p.ws, p.n, p.out_dtype, p.residual, p.out, p.combined, p.q, p.scale, p.maxima,
+                     p.normed);
   return hipGetLastError();
 }
 
+// Rows per workgroup: 16 (8 streaming waves) up to N = 4096, 24 (12) beyond,
+// so that the o (4096) and qkv (6144) projections run one workgroup per CU.
 template <int PROD>
 static hipError_t launch_produce_epi(hipStream_t st, const ProduceArgs& p) {
-  // Four rows per wave up to N = 8192, one beyond.  Each workgroup repeats
-  // the producer, so fewer workgroups pay less for it than the plain GEMV's
-  // two rows per wave would: measured on MI355X, graphs of 24 distinct-weight
-  // launches, two -> four rows, quantize + o with residual (4096 x 4096)
-  // 5.50 -> 4.90 us, norm_quantize + qkv (6144 x 4096) 7.75 -> 7.56.
   if (p.residual)
-    return p.n <= 8192 ? launch_produce<4, EPI_RESIDUAL, PROD>(st, p) : launch_produce<1, EPI_RESIDUAL, PROD>(st, p);
-  return p.n <= 8192 ? launch_produce<4, EPI_PLAIN, PROD>(st, p) : launch_produce<1, EPI_PLAIN, PROD>(st, p);
+    return p.n <= 4096 ? launch_split<8, 2, EPI_RESIDUAL, PROD>(st, p) : launch_split<12, 2, EPI_RESIDUAL, PROD>(st, p);
+  return p.n <= 4096 ? launch_split<8, 2, EPI_PLAIN, PROD>(st, p) : launch_split<12, 2, EPI_PLAIN, PROD>(st, p);
 }
 
 hipError_t launch_gemv_produce(hipStream_t st, const ProduceArgs& p) {
@@ -1048,10 +1179,11 @@ hipError_t launch_gemv_swiglu(hipStream_t st, const SwigluArgs& a) {
 
 hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a, bool row_tail) {
   if (a.n == 0 || a.k != 4096 || !a.maxima) return hipErrorInvalidValue;
-  constexpr int RC = 2;  // four coordinates per wave: 20.5 us against 18.8 (gate_up 2 x 12288 x 4096)
-  const dim3 grid((a.n + RC * kGemvWaves - 1) / (RC * kGemvWaves));
-  hipLaunchKernelGGL(gemv_swiglu_norm<RC>, grid, dim3(kGemvThreads), 0, st, p.x, p.gain, a.wg, a.wsg, a.wu, a.wsu,
-                     a.n, a.out_dtype, a.gate, a.up, a.act, p.q, p.scale, p.maxima, p.normed);
+  // 12 streaming waves of 4 coordinates: one workgroup per CU for 12,288
+  constexpr int NS = 12, CS = 4;
+  const dim3 grid((a.n + NS * CS - 1) / (NS * CS));
+  hipLaunchKernelGGL((gemv_swiglu_split<NS, CS>), grid, dim3((NS + kProdWaves) * kWave), 0, st, p.x, p.gain, a.wg,
+                     a.wsg, a.wu, a.wsu, a.n, a.out_dtype, a.gate, a.up, a.act, p.q, p.scale, p.maxima, p.normed);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !row_tail) return e;
   // the norm reset maxima[0] inside the GEMV; the row tail folds into it
@@ -1060,16 +1192,22 @@ hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const S
   return hipGetLastError();
 }
 
+template <int EPI, bool BF16_ACT>
+static hipError_t launch_rowtail(hipStream_t st, const RowtailArgs& d) {
+  // 8 streaming waves of 2 rows: one workgroup per CU for N = 4096
+  constexpr int NS = 8, RS = 2;
+  const dim3 grid((d.n + NS * RS - 1) / (NS * RS)), block((NS + kProdWaves) * kWave);
+  hipLaunchKernelGGL((gemv_rowtail_split<NS, RS, EPI, BF16_ACT>), grid, block, 0, st, d.act, d.maxima, d.w, d.ws,
+                     d.n, d.out_dtype, d.residual, d.out, d.combined, d.q_out, d.scale_out);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_rowtail(hipStream_t st, const RowtailArgs& d) {
   if (d.n == 0 || !d.maxima) return hipErrorInvalidValue;
-  const dim3 grid((d.n + kRowtailWaves - 1) / kRowtailWaves), block(kRowtailWaves * kWave);
+  const bool bf16 = d.act_dtype == W8A8_OUT_BF16;
   if (d.residual)
-    hipLaunchKernelGGL(gemv_m1_rowtail<EPI_RESIDUAL>, grid, block, 0, st, d.act, d.act_dtype, d.maxima, d.w, d.ws,
-                       d.n, d.out_dtype, d.residual, d.out, d.combined, d.q_out, d.scale_out);
-  else
-    hipLaunchKernelGGL(gemv_m1_rowtail<EPI_PLAIN>, grid, block, 0, st, d.act, d.act_dtype, d.maxima, d.w, d.ws,
-                       d.n, d.out_dtype, nullptr, d.out, nullptr, d.q_out, d.scale_out);
-  return hipGetLastError();
+    return bf16 ? launch_rowtail<EPI_RESIDUAL, true>(st, d) : launch_rowtail<EPI_RESIDUAL, false>(st, d);
+  return bf16 ? launch_rowtail<EPI_PLAIN, true>(st, d) : launch_rowtail<EPI_PLAIN, false>(st, d);
 }
 
 hipError_t launch_swiglu_quantize_rows(hipStream_t st, const void* act, size_t rows, uint32_t width, int dtype,
