@@ -71,6 +71,19 @@ __device__ __forceinline__ uint32_t wave_id() {
   return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
+// The row slot of workgroup b among G.  The dispatcher deals workgroups to
+// the eight XCDs in turn (b on XCD b mod 8); slot (b mod 8) (G / 8) + b / 8
+// gives each XCD a contiguous range of slots, so that at each step an XCD's
+// streaming waves read consecutive rows, spread over the HBM channels,
+// instead of every eighth row.  Measured on MI355X with per-workgroup clock
+// stamps: with slot = b, one XCD's workgroups ended up to 2 us after
+// another's in the 12,288-coordinate SwiGLU GEMV.  (The dispatcher-ordered
+// GEMVs keep slot = b: this mapping made the decode chain of gemv_m1_one
+// launches 1.306 -> 1.327 ms.)
+__device__ __forceinline__ uint32_t xcd_slot(uint32_t b, uint32_t G) {
+  return G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
+}
+
 __device__ __forceinline__ void store_out(void* out, size_t idx, int dtype, int32_t acc, float value) {
   if (dtype == W8A8_OUT_F32)
     reinterpret_cast<float*>(out)[idx] = value;
@@ -593,17 +606,6 @@ struct SplitLds {
   float scale;
   alignas(16) int8_t qs[K];
 };
-
-// The row slot of workgroup b among G.  The dispatcher deals workgroups to
-// the eight XCDs in turn (b on XCD b mod 8); slot (b mod 8) (G / 8) + b / 8
-// gives each XCD a contiguous range of slots, so that at each step an XCD's
-// streaming waves read consecutive rows, spread over the HBM channels,
-// instead of every eighth row.  Measured on MI355X with per-workgroup clock
-// stamps: with slot = b, one XCD's workgroups ended up to 2 us after
-// another's in the 12,288-coordinate SwiGLU GEMV.
-__device__ __forceinline__ uint32_t xcd_slot(uint32_t b, uint32_t G) {
-  return G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
-}
 
 // Workgroup barrier that orders the LDS operations before it and nothing
 // else: a wave's outstanding global loads stay in flight across it.
