@@ -772,28 +772,41 @@ def main() -> int:
     return 0
 
 
+C2_NAME = "C2 decode layers 0-3: qkv, o, gate_up, down at M=1"
+
+
 def cpu_baseline() -> dict:
     """The C oracle (quantize + exact integer GEMV/GEMM + epilogue, OpenMP
     over output channels; argmax for the head) timed on this host on every
-    BASELINE config, each at all host cores (at most 16), 8 threads (the
-    reference fixture's setting, tools/operator_fixtures.py:17) and 1 thread.
-    Samples: C1 one 4096x4096 projection; C2 layer 0's four projections;
-    C3 the whole 151,936-row head with argmax; C4 the o shape (4096x4096) at
-    M = 129 and 512 on Student-t rows; C5 the down shape (4096x12288) at
-    M = 4, 16 and 64 on per-row-seeded rows.  `value` is C2 at all cores."""
+    BASELINE config, each at all the cores this process may use, 8 threads
+    (the reference fixture's setting, tools/operator_fixtures.py:17) and 1
+    thread; median of 5 or more runs after one warmup run.  "All cores" is
+    nproc, capped by OMP_NUM_THREADS when that is set (the GPU box sets it to
+    its one-GPU share of the host); the cap is reported.  Samples: C1 one
+    4096x4096 projection; C2 four decode layers' sixteen projections
+    (layers 0-3, 772 MB of weights: larger than any host L3, so the figure is
+    a DRAM rate); C3 the whole 151,936-row head with argmax; C4 the o shape
+    (4096x4096) at M = 129 and 512 on Student-t rows; C5 the down shape
+    (4096x12288) at M = 4, 16 and 64 on per-row-seeded rows.  `value` is C2
+    at all cores."""
     import oracle
     from inferrous_amd import synth
 
     t0 = time.time()
-    nthreads = max(1, min(os.cpu_count() or 1, 16))
+    nproc = os.cpu_count() or 1
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    nthreads = max(1, min(nproc, cap) if cap > 0 else nproc)
     thread_counts = sorted({nthreads, 8, 1}, reverse=True)
+    c2_layers = 4
 
     def weights(layer: int, si: int):
         _, n, k = synth.DECODE_SHAPES[si]
         return (oracle.synth_i8(SEED_W, synth.weight_stream(layer, si), 0, n * k),
                 oracle.synth_f32(SEED_S, synth.scale_stream(layer, si), 0, n, 1e-3, 1e-2))
 
-    mats = [(n, k) + weights(0, si) for si, (_, n, k) in enumerate(synth.DECODE_SHAPES)]
+    layer_mats = [[(n, k) + weights(layer, si) for si, (_, n, k) in enumerate(synth.DECODE_SHAPES)]
+                  for layer in range(c2_layers)]
+    mats = layer_mats[0]
     xs = {4096: synth.normal_rows(40, 1, 4096).reshape(-1), 12288: synth.normal_rows(41, 1, 12288).reshape(-1)}
     hn, hk = synth.VOCAB, synth.HIDDEN
     hw = oracle.synth_i8(SEED_W, 9001, 0, hn * hk)
@@ -809,9 +822,10 @@ def cpu_baseline() -> dict:
     # (name, algorithmic bytes, integer ops 2*M*N*K, pass at `threads`)
     configs = [("C1 linear M=1 4096x4096", gemv_bytes(4096, 4096), 2 * 4096 * 4096,
                 lambda th: linear_pass(xs[4096], 1, 4096, 4096, wo, so, th)),
-               ("C2 decode layer 0: qkv, o, gate_up, down at M=1",
-                sum(gemv_bytes(n, k) for (n, k, _, _) in mats), sum(2 * n * k for (n, k, _, _) in mats),
-                lambda th: [linear_pass(xs[k], 1, n, k, w, ws, th) for (n, k, w, ws) in mats]),
+               (C2_NAME,
+                c2_layers * sum(gemv_bytes(n, k) for (n, k, _, _) in mats),
+                c2_layers * sum(2 * n * k for (n, k, _, _) in mats),
+                lambda th: [linear_pass(xs[k], 1, n, k, w, ws, th) for lm in layer_mats for (n, k, w, ws) in lm]),
                ("C3 lm_head 151936x4096 + argmax, M=1", gemv_bytes(hn, hk, out_bytes=0) + 4, 2 * hn * hk,
                 lambda th: oracle.linear_argmax(*oracle.quantize(xh, hk), hw, hs, hk, threads=th))]
     for m in (129, 512):
@@ -824,10 +838,10 @@ def cpu_baseline() -> dict:
                         lambda th, x=x, m=m: linear_pass(x, m, 4096, 12288, wd, sd, th)))
 
     def median_seconds(fn) -> float:
-        fn()
+        fn()  # warmup
         times = []
         start = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - start < 0.6 and len(times) < 9):
+        while len(times) < 5 or (time.perf_counter() - start < 0.6 and len(times) < 9):
             t = time.perf_counter()
             fn()
             times.append(time.perf_counter() - t)
@@ -850,13 +864,15 @@ def cpu_baseline() -> dict:
                 break
     except OSError:
         pass
-    c2 = per["C2 decode layer 0: qkv, o, gate_up, down at M=1"]["GB/s_by_threads"]
+    c2 = per[C2_NAME]["GB/s_by_threads"]
+    c2_mb = c2_layers * sum(gemv_bytes(n, k) for (n, k, _, _) in mats) / 1e6
     return {"value": c2[str(nthreads)], "unit": "GB/s", "cores": nthreads, "kind": "port",
-            "sample": (f"C oracle (quantize + int32 GEMV/GEMM + BF16 epilogue; argmax for C3), median of >=3 "
-                       f"runs per point; value = C2 (layer 0's four decode projections at M=1, "
-                       f"{sum(gemv_bytes(n, k) for (n, k, _, _) in mats) / 1e6:.1f} MB) at {nthreads} threads; "
-                       f"{cpu_model}, {os.cpu_count()} logical CPUs"),
-            "cpu_model": cpu_model, "logical_cpus": os.cpu_count(),
+            "sample": (f"C oracle (quantize + int32 GEMV/GEMM + BF16 epilogue; argmax for C3), median of >=5 "
+                       f"runs after 1 warmup per point; value = C2 (decode layers 0-{c2_layers - 1}, 16 projections "
+                       f"at M=1, {c2_mb:.1f} MB of weights) at {nthreads} threads; {cpu_model}, {nproc} logical CPUs"
+                       + (f", threads capped at OMP_NUM_THREADS={cap}" if 0 < cap < nproc else "")),
+            "cpu_model": cpu_model, "logical_cpus": nproc,
+            "thread_cap": {"OMP_NUM_THREADS": cap or None, "applied": bool(0 < cap < nproc)},
             "per_config": per}
 
 

@@ -2,10 +2,10 @@
 W8A8 baseline), on the same seeded synthetic tensors the bench uses.
 
 Weights are generated on the device; the checker regenerates the same rows
-on the host (oracle.synth_*), so full matrices are compared where the CPU
-oracle finishes in seconds (every output of the 36-layer decode set and of
-the lm_head) and sampled rows plus a row-sum identity for the prefill
-shapes.
+on the host (oracle.synth_*) and compares every output: the 36-layer decode
+set, the lm_head, every row of the four prefill shapes at M = 129 and 512
+(the threaded C oracle runs those 198 G int8 ops in about a second), and
+the ragged small-M batches.
 """
 from __future__ import annotations
 
@@ -125,9 +125,9 @@ def test_config3_lm_head_argmax_full(env):
 @pytest.mark.parametrize("m", [129, 512])
 def test_config4_prefill_shapes(env, m):
     """Student-t(3) activations with 8 x50 outlier channels, per-token
-    quantization, then the MFMA GEMM on all four layer shapes."""
+    quantization, then the MFMA GEMM on all four layer shapes: every row of
+    the i32 accumulators and of the BF16 outputs against the oracle."""
     ctx, mod, s = env
-    rng = np.random.default_rng(m)
     for si, (name, n, k) in enumerate(synth.DECODE_SHAPES):
         x = synth.student_t_rows(700 + si, m, k)
         q, sc, hq, hsc = quantize_dev(mod, s, x, k)
@@ -139,13 +139,11 @@ def test_config4_prefill_shapes(env, m):
         acc = o32.to_host_vec(s).reshape(m, n)
         outb = ob.to_host_vec(s).reshape(m, n)
         hw, hws = host_weights(n, k, 5000 + si, 5100 + si)
-        rsel = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 10)]))
-        a2, _, b2 = oracle.linear(hq[rsel], hsc[rsel], hw, hws, k)
-        assert np.array_equal(acc[rsel], a2.reshape(len(rsel), n)), name
-        assert np.array_equal(outb[rsel], b2.reshape(len(rsel), n)), name
-        # every row: sum_c acc[r, c] == q[r] . colsum(W)
-        col = hw.astype(np.int64).sum(0)
-        assert np.array_equal(acc.astype(np.int64).sum(1), hq.astype(np.int64) @ col), name
+        a2, _, b2 = oracle.linear(hq, hsc, hw, hws, k)
+        bad = np.flatnonzero((acc != a2.reshape(m, n)).any(1))
+        assert bad.size == 0, f"{name}: {bad.size} rows of acc differ, first row {bad[:1]}"
+        bad = np.flatnonzero((outb != b2.reshape(m, n)).any(1))
+        assert bad.size == 0, f"{name}: {bad.size} rows of the BF16 output differ, first row {bad[:1]}"
 
 
 @pytest.mark.parametrize("m", [4, 16, 64])
