@@ -944,6 +944,80 @@ int w8a8_diag_linear_timeline(void* stream, const int8_t* q, const float* asc, c
                                          stamps));
 }
 
+// Fixed layout of a route record (include/inferrous_w8a8_diag.h).
+static void put_route(int32_t* r, int family, uint32_t gx, uint32_t gy, uint32_t block) {
+  for (size_t i = 0; i < W8A8_DIAG_ROUTE_LEN; ++i) r[i] = 0;
+  r[0] = family;
+  r[1] = (int32_t)gx;
+  r[2] = (int32_t)gy;
+  r[3] = (int32_t)block;
+}
+
+static void put_gemv_route(int32_t* r, const GemvRoute& g) {
+  put_route(r, g.family, g.grid_x, g.grid_y, 64u * (uint32_t)g.waves);
+  r[11] = g.mt;
+  r[13] = g.u;
+  r[17] = g.rows;
+  r[18] = g.kc;
+  r[19] = g.waves;
+}
+
+int w8a8_diag_linear_route(size_t m, size_t n, uint32_t k, int out_dtype, int residual, int path,
+                           size_t workspace_bytes, int32_t* route, size_t route_len) {
+  if (!route) return W8A8_ENULL;
+  if (route_len < W8A8_DIAG_ROUTE_LEN) return W8A8_EWORKSPACE;
+  if (out_dtype != W8A8_OUT_I32 && out_dtype != W8A8_OUT_F32 && out_dtype != W8A8_OUT_BF16) return W8A8_EARG;
+  if (path != W8A8_PATH_AUTO && path != W8A8_PATH_DOT4 && path != W8A8_PATH_MFMA) return W8A8_EARG;
+  if (k == 0 || k % 16 != 0 || m > kU32Max || n > kU32Max) return W8A8_ESHAPE;
+  if (residual && out_dtype == W8A8_OUT_I32) return W8A8_EARG;
+  put_route(route, kRouteNone, 0, 0, 0);
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (path == W8A8_PATH_AUTO) path = auto_path(m, n, k, workspace_bytes);
+  if (path == W8A8_PATH_DOT4) {
+    const uint32_t nn = (uint32_t)n;
+    put_gemv_route(route, gemv_route((uint32_t)m, k, &nn, 1, false));
+    return W8A8_OK;
+  }
+  // the route taken with 16-byte aligned operands and a workspace of
+  // workspace_bytes (a non-null stand-in: only its presence and size count)
+  static const float kDummy[4] = {0.f, 0.f, 0.f, 0.f};
+  GemmArgs a{};
+  a.m = (uint32_t)m;
+  a.n = (uint32_t)n;
+  a.k = k;
+  a.out_dtype = out_dtype;
+  a.residual = residual ? kDummy : nullptr;
+  a.partials = workspace_bytes ? (int32_t*)kDummy : nullptr;
+  a.partial_bytes = workspace_bytes;
+  const GemmRoute g = gemm_route(a);
+  put_route(route, g.family, g.grid_x, g.grid_y, g.block);
+  route[4] = g.bm;
+  route[5] = g.bn;
+  route[6] = g.wm;
+  route[7] = g.wn;
+  route[8] = g.sa;
+  route[9] = g.sb;
+  route[10] = g.ma;
+  route[11] = g.mt;
+  route[12] = g.s;
+  route[13] = g.u;
+  route[14] = (int32_t)g.splits;
+  route[15] = g.nt_slabs;
+  route[16] = g.epi_cols;
+  return W8A8_OK;
+}
+
+int w8a8_diag_argmax_route(size_t n, uint32_t k, int32_t* route, size_t route_len) {
+  if (!route) return W8A8_ENULL;
+  if (route_len < W8A8_DIAG_ROUTE_LEN) return W8A8_EWORKSPACE;
+  if (k == 0 || k % 16 != 0 || n > kU32Max) return W8A8_ESHAPE;
+  put_route(route, kRouteNone, 0, 0, 0);
+  if (n == 0) return W8A8_OK;
+  const uint32_t nn = (uint32_t)n;
+  put_gemv_route(route, gemv_route(1, k, &nn, 1, true));
+  return W8A8_OK;
+}
+
 int w8a8_synth_i8(void* stream, int8_t* out, size_t n, uint64_t seed, uint64_t stream_id) {
   if (n == 0) return W8A8_OK;
   if (!out) return W8A8_ENULL;

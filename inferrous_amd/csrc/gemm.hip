@@ -1032,21 +1032,25 @@ static void launch_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits, 
                        a.partials, splits);
 }
 
+// 8 columns per split-K epilogue thread above M = 200 when every row of
+// every operand starts 16-byte aligned (n % 8 == 0 and aligned bases); 4
+// otherwise.  The epilogue is latency-bound: up to M = 200 twice the threads
+// with half the loads each finish sooner.  Measured on MI355X, graphs of 16
+// distinct-weight launches, GEMM + epilogue, 8 -> 4 columns: M = 64 o
+// 10.3 -> 9.7 us, M = 100 qkv 14.4 -> 13.5, M = 129 qkv 15.6-15.8 -> 14.9,
+// o 13.5-13.9 -> 13.1, down 22.6-24.1 -> 22.0, M = 200 qkv 18.7 -> 17.7;
+// but M = 255 o 15.9-16.1 -> 17.1, and level on gemm_dma's split route at
+// M = 300 and 512.
+static bool wide_epilogue(const GemmArgs& a) {
+  return a.m > 200 && a.n % 8 == 0 && aligned16(a.partials) && aligned16(a.out) &&
+         (a.out_dtype == W8A8_OUT_I32 || aligned16(a.ws)) &&
+         (!a.residual || (aligned16(a.residual) && aligned16(a.combined)));
+}
+
 template <bool NT>
 static hipError_t launch_splitk_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits) {
   if (splits < 1 || splits > kMaxSplits) return hipErrorInvalidValue;
-  // 8 columns per thread above M = 200 when every row of every operand
-  // starts 16-byte aligned (n % 8 == 0 and aligned bases); 4 otherwise.  The
-  // epilogue is latency-bound: up to M = 200 twice the threads with half the
-  // loads each finish sooner.  Measured on MI355X, graphs of 16
-  // distinct-weight launches, GEMM + epilogue, 8 -> 4 columns: M = 64 o
-  // 10.3 -> 9.7 us, M = 100 qkv 14.4 -> 13.5, M = 129 qkv 15.6-15.8 -> 14.9,
-  // o 13.5-13.9 -> 13.1, down 22.6-24.1 -> 22.0, M = 200 qkv 18.7 -> 17.7;
-  // but M = 255 o 15.9-16.1 -> 17.1, and level on gemm_dma's split route at
-  // M = 300 and 512.
-  const bool wide = a.m > 200 && a.n % 8 == 0 && aligned16(a.partials) && aligned16(a.out) &&
-                    (a.out_dtype == W8A8_OUT_I32 || aligned16(a.ws)) &&
-                    (!a.residual || (aligned16(a.residual) && aligned16(a.combined)));
+  const bool wide = wide_epilogue(a);
   if (a.out_dtype == W8A8_OUT_I32)
     launch_epilogue<EP_I32, NT>(st, a, splits, wide);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
@@ -1106,9 +1110,14 @@ static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits
 }
 
 // ---------------------------------------------------------------- dispatch
-hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
-  if (a.m == 0 || a.n == 0) return hipSuccess;
-  const unsigned nb16 = (a.n + 15) / 16;
+// The route of one GEMM call (see GemmRoute).
+GemmRoute gemm_route(const GemmArgs& a) {
+  GemmRoute r{};
+  r.splits = 1;
+  r.epi_cols = 4;
+  r.grid_y = 1;
+  r.block = 512;
+  if (a.m == 0 || a.n == 0) return r;
   // m <= 256 goes to gemm_tall when its plan applies.
   // Otherwise, for small m: from m = 8 the 8-wave kernel with 64-row tiles
   // streams the weights faster when n gives at least 128 tiles; below that
@@ -1133,44 +1142,99 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
       // M = 200 33.7-35.1 -> 31.5-32.9 us, M = 255 37.6-37.9 -> 36.1-37.1
       // from 3 / 3), 3 / 3 and 4 / 4 for the split routes (2 / 3, 2 / 4 and
       // 3 / 4 level or slower there).
-      if (ma == 64)
-        return tile == 96 ? launch_tall<96, 4, 4, 64>(st, a, splits) : launch_tall<64, 4, 4, 64>(st, a, splits);
-      if (ma == 160)
-        return tile == 96 ? launch_tall<96, 4, 4, 160>(st, a, splits) : launch_tall<64, 4, 4, 160>(st, a, splits);
-      if (tile == 96)
-        return splits > 1 ? launch_tall<96, 3, 3, 256>(st, a, splits) : launch_tall<96, 2, 4, 256>(st, a, splits);
-      return launch_tall<64, 4, 4, 256>(st, a, splits);
+      r.family = kRouteTall;
+      r.bn = tile;
+      r.ma = ma;
+      r.splits = splits;
+      r.sa = r.sb = 4;
+      if (ma == 256 && tile == 96) {
+        r.sa = splits > 1 ? 3 : 2;
+        r.sb = splits > 1 ? 3 : 4;
+      }
+      r.grid_x = (a.n + tile - 1) / tile * splits;
+      if (splits > 1) {
+        r.nt_slabs = stream_slabs(a, splits);
+        r.epi_cols = wide_epilogue(a) ? 8 : 4;
+      }
+      return r;
     }
   }
-  if (a.m <= 16 && !wide) {
-    hipLaunchKernelGGL((gemm_skinny<1, 4, 4>), dim3(nb16, 1), dim3(256), 0, st, a);
-  } else if (a.m <= 32 && !wide) {
-    hipLaunchKernelGGL((gemm_skinny<2, 4, 4>), dim3(nb16, 1), dim3(256), 0, st, a);
-  } else if (a.m <= 64 && !wide) {
-    hipLaunchKernelGGL((gemm_skinny<4, 4, 2>), dim3(nb16, 1), dim3(256), 0, st, a);
-  } else if (a.k % 128 == 0) {
+  const uint32_t nb16 = (a.n + 15) / 16;
+  if (a.m <= 64 && !wide) {
+    r.family = kRouteSkinny;
+    r.mt = a.m <= 16 ? 1 : a.m <= 32 ? 2 : 4;
+    r.s = 4;
+    r.u = a.m <= 32 ? 4 : 2;
+    r.grid_x = nb16;
+    r.block = 64 * r.s;
+    return r;
+  }
+  if (a.k % 128 == 0) {
+    r.family = kRouteDma;
     uint32_t splits;
     if (a.partials && split_plan(a.m, a.n, a.k, splits) &&
-        a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t))
-      return launch_split<128, 128, 32, 64, 4, 4>(st, a, splits);
-    // Tile per problem, measured on MI355X at M = 129 / 512 on the Qwen3-8B
-    // projection shapes: the largest tile that still gives about one tile
-    // per CU, smaller tiles for narrow N.
-    // Residual outputs skip the 256 x 192 tile (kResidualTile); t128 is
-    // then at least 480.
-    const uint64_t t256 = (uint64_t)((a.m + 255) / 256) * ((a.n + 191) / 192);
-    const uint64_t t128 = (uint64_t)((a.m + 127) / 128) * ((a.n + 191) / 192);
-    if (t256 >= 240 && !a.residual) return launch_dma<256, 192, 64, 96, 2, 3>(st, a);
-    if (t128 >= 240) return launch_dma<128, 192, 32, 96, 2, 4>(st, a);
-    if (a.n >= 6144 && a.m >= 256) return launch_dma<128, 128, 32, 64, 4, 4>(st, a);
-    if (a.m >= 128) return launch_dma<128, 64, 32, 32, 4, 4>(st, a);
-    return launch_dma<64, 128, 32, 32, 4, 4>(st, a);
-  } else {
-    constexpr int BM = 128, BN = 128;
-    const uint32_t tm = (a.m + BM - 1) / BM, tn = (a.n + BN - 1) / BN;
-    hipLaunchKernelGGL((gemm_tiled<BM, BN, 64, 64>), dim3(tm * tn), dim3(256), 0, st, a, tm, tn);
+        a.partial_bytes >= (size_t)splits * a.m * a.n * sizeof(int32_t)) {
+      r.bm = 128, r.bn = 128, r.wm = 32, r.wn = 64, r.sa = 4, r.sb = 4;
+      r.splits = splits;
+      r.epi_cols = wide_epilogue(a) ? 8 : 4;
+    } else {
+      // Tile per problem, measured on MI355X at M = 129 / 512 on the Qwen3-8B
+      // projection shapes: the largest tile that still gives about one tile
+      // per CU, smaller tiles for narrow N.  Residual outputs skip the
+      // 256 x 192 tile (kResidualTile); t128 is then at least 480.
+      const uint64_t t256 = (uint64_t)((a.m + 255) / 256) * ((a.n + 191) / 192);
+      const uint64_t t128 = (uint64_t)((a.m + 127) / 128) * ((a.n + 191) / 192);
+      if (t256 >= 240 && !a.residual) r.bm = 256, r.bn = 192, r.wm = 64, r.wn = 96, r.sa = 2, r.sb = 3;
+      else if (t128 >= 240) r.bm = 128, r.bn = 192, r.wm = 32, r.wn = 96, r.sa = 2, r.sb = 4;
+      else if (a.n >= 6144 && a.m >= 256) r.bm = 128, r.bn = 128, r.wm = 32, r.wn = 64, r.sa = 4, r.sb = 4;
+      else if (a.m >= 128) r.bm = 128, r.bn = 64, r.wm = 32, r.wn = 32, r.sa = 4, r.sb = 4;
+      else r.bm = 64, r.bn = 128, r.wm = 32, r.wn = 32, r.sa = 4, r.sb = 4;
+    }
+    r.grid_x = (a.m + r.bm - 1) / r.bm * ((a.n + r.bn - 1) / r.bn) * r.splits;
+    return r;
   }
-  return hipGetLastError();
+  r.family = kRouteTiled;
+  r.bm = 128, r.bn = 128, r.wm = 64, r.wn = 64;
+  r.grid_x = (a.m + r.bm - 1) / r.bm * ((a.n + r.bn - 1) / r.bn);
+  r.block = 256;
+  return r;
+}
+
+hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
+  const GemmRoute r = gemm_route(a);
+  auto is = [&](int bm, int bn, int wm, int wn, int sa, int sb) {
+    return r.bm == bm && r.bn == bn && r.wm == wm && r.wn == wn && r.sa == sa && r.sb == sb;
+  };
+  switch (r.family) {
+    case kRouteNone:
+      return hipSuccess;
+    case kRouteTall:
+      if (r.ma == 64)
+        return r.bn == 96 ? launch_tall<96, 4, 4, 64>(st, a, r.splits) : launch_tall<64, 4, 4, 64>(st, a, r.splits);
+      if (r.ma == 160)
+        return r.bn == 96 ? launch_tall<96, 4, 4, 160>(st, a, r.splits) : launch_tall<64, 4, 4, 160>(st, a, r.splits);
+      if (r.bn == 96)
+        return r.splits > 1 ? launch_tall<96, 3, 3, 256>(st, a, r.splits) : launch_tall<96, 2, 4, 256>(st, a, r.splits);
+      return launch_tall<64, 4, 4, 256>(st, a, r.splits);
+    case kRouteSkinny:
+      if (r.mt == 1) hipLaunchKernelGGL((gemm_skinny<1, 4, 4>), dim3(r.grid_x, 1), dim3(r.block), 0, st, a);
+      else if (r.mt == 2) hipLaunchKernelGGL((gemm_skinny<2, 4, 4>), dim3(r.grid_x, 1), dim3(r.block), 0, st, a);
+      else hipLaunchKernelGGL((gemm_skinny<4, 4, 2>), dim3(r.grid_x, 1), dim3(r.block), 0, st, a);
+      return hipGetLastError();
+    case kRouteDma:
+      if (r.splits > 1) return launch_split<128, 128, 32, 64, 4, 4>(st, a, r.splits);
+      if (is(256, 192, 64, 96, 2, 3)) return launch_dma<256, 192, 64, 96, 2, 3>(st, a);
+      if (is(128, 192, 32, 96, 2, 4)) return launch_dma<128, 192, 32, 96, 2, 4>(st, a);
+      if (is(128, 128, 32, 64, 4, 4)) return launch_dma<128, 128, 32, 64, 4, 4>(st, a);
+      if (is(128, 64, 32, 32, 4, 4)) return launch_dma<128, 64, 32, 32, 4, 4>(st, a);
+      return launch_dma<64, 128, 32, 32, 4, 4>(st, a);
+    case kRouteTiled: {
+      const uint32_t tm = (a.m + 127) / 128, tn = (a.n + 127) / 128;
+      hipLaunchKernelGGL((gemm_tiled<128, 128, 64, 64>), dim3(tm * tn), dim3(256), 0, st, a, tm, tn);
+      return hipGetLastError();
+    }
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace w8a8

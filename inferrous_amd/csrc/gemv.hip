@@ -1059,21 +1059,46 @@ static hipError_t launch_mt(hipStream_t st, GemvArgs& a, const uint32_t* nn, uin
 
 // Row-group shape: measured on MI355X, waves that issue one short batch
 // (one or two 4 KiB rows) and exit stream HBM better than longer batches or
-// grid-stride sweeps; two rows per wave helps only the small matrices.
+// grid-stride sweeps; two rows per wave helps only the small matrices.  M = 1
+// at K = 4096 / 12288: gemv_m1_one (one matrix) or gemv_m1 (siblings, or the
+// fused selection, whose workgroups carry 16 waves: a quarter of the keys of
+// the plain GEMV's 4-wave workgroups).  Otherwise gemv_mt with 4-row groups.
+GemvRoute gemv_route(uint32_t m, uint32_t k, const uint32_t* n, int count, bool argmax) {
+  GemvRoute r{};
+  uint64_t total = 0;
+  for (int i = 0; i < count; ++i) total += n[i];
+  r.grid_y = 1;
+  if (m == 1 && (k == 4096 || k == 12288)) {
+    r.family = argmax || count != 1 ? kRouteGemvM1 : kRouteGemvM1One;
+    r.rows = k == 4096 && total <= 8192 ? 2 : 1;
+    r.kc = (int)(k / 1024);
+    r.waves = argmax ? 16 : kGemvWaves;
+  } else {
+    r.family = kRouteGemvMt;
+    r.rows = 4;
+    r.mt = (m == 1 || argmax) ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    r.u = r.mt <= 2 ? 4 : 2;
+    r.waves = kGemvWaves;
+    r.grid_y = (m + r.mt - 1) / r.mt;
+  }
+  uint64_t groups = 0;
+  for (int i = 0; i < count; ++i) groups += (n[i] + r.rows - 1) / r.rows;
+  r.grid_x = (uint32_t)((groups + r.waves - 1) / r.waves);
+  return r;
+}
+
 template <int EPI>
 static hipError_t dispatch(hipStream_t st, GemvArgs& a, uint32_t* blocks) {
+  const GemvRoute r = gemv_route(a.m, a.k, a.n, a.count, EPI == EPI_ARGMAX);
   uint32_t nn[kMaxGroup];
-  uint64_t total = 0;
-  for (int i = 0; i < a.count; ++i) {
-    nn[i] = a.n[i];
-    total += a.n[i];
+  for (int i = 0; i < a.count; ++i) nn[i] = a.n[i];
+  if (r.family != kRouteGemvMt) {
+    if (r.kc == 12) return launch_m1<1, 12, EPI>(st, a, nn, blocks);
+    return r.rows == 2 ? launch_m1<2, 4, EPI>(st, a, nn, blocks) : launch_m1<1, 4, EPI>(st, a, nn, blocks);
   }
-  if (a.m == 1 && a.k == 4096)
-    return total <= 8192 ? launch_m1<2, 4, EPI>(st, a, nn, blocks) : launch_m1<1, 4, EPI>(st, a, nn, blocks);
-  if (a.m == 1 && a.k == 12288) return launch_m1<1, 12, EPI>(st, a, nn, blocks);
-  if (a.m == 1 || EPI == EPI_ARGMAX) return launch_mt<1, 4, EPI>(st, a, nn, blocks);
-  if (a.m <= 2) return launch_mt<2, 4, EPI>(st, a, nn, blocks);
-  if (a.m <= 4) return launch_mt<4, 2, EPI>(st, a, nn, blocks);
+  if (r.mt == 1) return launch_mt<1, 4, EPI>(st, a, nn, blocks);
+  if (r.mt == 2) return launch_mt<2, 4, EPI>(st, a, nn, blocks);
+  if (r.mt == 4) return launch_mt<4, 2, EPI>(st, a, nn, blocks);
   return launch_mt<8, 2, EPI>(st, a, nn, blocks);
 }
 

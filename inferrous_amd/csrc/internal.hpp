@@ -70,6 +70,34 @@ struct GemmArgs {
 // Bytes of split-K workspace launch_gemm would use for this shape (0: none).
 size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 
+// The launch a GEMM call makes, decided on the host: the kernel family, its
+// compile-time shape and its grid.  launch_gemm runs exactly this route; the
+// diagnostics export it so that host-side checks can replay each kernel's
+// index arithmetic over its grid.
+enum { kRouteNone = 0, kRouteGemvM1One = 1, kRouteGemvM1 = 2, kRouteGemvMt = 3, kRouteSkinny = 11,
+       kRouteTall = 12, kRouteDma = 13, kRouteTiled = 14 };
+struct GemmRoute {
+  int family;                       // kRouteSkinny, kRouteTall, kRouteDma, kRouteTiled (kRouteNone: m or n is 0)
+  int bm, bn, wm, wn, sa, sb, ma;   // dma / tiled tile; tall: bn, sa, sb, ma
+  int mt, s, u;                     // skinny: 16-row tiles, waves, unroll
+  uint32_t splits;                  // split-K slabs (1: none)
+  int nt_slabs;                     // slabs streamed (EP_SLAB)
+  int epi_cols;                     // split-K epilogue columns per thread (4 or 8)
+  uint32_t grid_x, grid_y, block;   // the GEMM launch
+};
+GemmRoute gemm_route(const GemmArgs& a);
+
+// The launch a GEMV call makes (launch_gemv / launch_gemv_argmax): family
+// kRouteGemvM1One, kRouteGemvM1 or kRouteGemvMt; `rows` rows per row group
+// (one wave's), kc = K / 1024 (M = 1 families), mt activation rows and u
+// chunks per pass (gemv_mt), waves per workgroup and the grid.
+struct GemvRoute {
+  int family;
+  int rows, kc, mt, u, waves;
+  uint32_t grid_x, grid_y;
+};
+GemvRoute gemv_route(uint32_t m, uint32_t k, const uint32_t* n, int count, bool argmax);
+
 hipError_t launch_quantize(hipStream_t st, const void* x, bool bf16, uint32_t width, size_t rows,
                            int8_t* q, float* scales, uint32_t* maxima_reset);
 hipError_t launch_quantize_with_max(hipStream_t st, const float* x, uint32_t width, size_t rows,
