@@ -579,6 +579,31 @@ def main() -> int:
                                  "GB/s": round(gemv_bytes(hn, hk, out_bytes=0) / (ms * 1e-3) / 1e9, 1)}
         extras["per_shape_gemv"] = per
         log(f"per shape: {per}")
+        # The same 145 projections as one launch (w8a8_linear_sequence: a
+        # device-wide barrier between dependent entries, weights requested
+        # ahead of it), against the graph of 146 launches above.
+        mod.sequence_reset()
+        seq_entries = [dict(q=qs[k][0], asc=qs[k][1], w=w, ws=ws, out=outs[name])
+                       for mats in layers for (name, n, k, w, ws) in mats]
+        seq_entries.append(dict(q=qs[hk][0], asc=qs[hk][1], w=head_w, ws=head_s, out=None, select=True))
+        plan = mod.prepare_sequence(seq_entries)
+        seq_token = DeviceBuffer.zeroed(s, 1, np.uint32)
+        for _ in range(20):
+            mod.linear_sequence(s, plan, seq_token)
+        s.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        for _ in range(50):
+            mod.linear_sequence(s, plan, seq_token)
+        e1.record(s)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / 50
+        seq_status = mod.sequence_status()
+        extras["decode_sequence_one_launch"] = {
+            "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1), "status": seq_status,
+            "token_matches_graph": int(seq_token.to_host_vec(s)[0]) == int(token.to_host_vec(s)[0]),
+            "entries": len(seq_entries)}
+        log(f"decode step as one sequence launch: {ms * 1e3:.1f} us (status {seq_status})")
         # step including a per-token quantize kernel before every projection
         ms = time_graph(capture(lambda: decode_step(with_quant=True)), 20)
         extras["decode_step_with_quantize"] = {"ms": round(ms, 4),
