@@ -363,6 +363,109 @@ def timeline_run() -> int:
     return 0
 
 
+def gemm_timeline_run() -> int:
+    """Where a gemm_tall launch spends its time (M = 129 on the four layer
+    shapes, the ragged M = 16 / 64 down and M = 16 gate_up), without a
+    profiler.  For each shape, 36 distinct-weight launches of
+    w8a8_diag_gemm_timeline (the kernel and launch of w8a8_linear_ex's
+    gemm_tall route with per-wave stamps of the 100 MHz clock, and the same
+    split-K slab epilogue launch) are captured as one graph and replayed 20
+    times; the last replay is read.  Per launch, medians of launches 2..35,
+    in us from the launch's first wave start: `prologue`, the median and the
+    last wave to have stage 0 of both rings landed; `stream`, the median and
+    the last wave to have issued its last MFMA (or DMA, for waves holding no
+    rows); `end`, the last store acknowledged; `between`, this launch's end to
+    the next launch's first wave (the slab epilogue launch and two launch
+    gaps for a split route, one gap otherwise); `period`, end to end.  The
+    per-CU pull model: each workgroup's (rows loaded + BN) x K range bytes
+    at 30 B/clk and the clock the stamps imply.  `plain us`: the same graph
+    through w8a8_linear_ex."""
+    from inferrous_amd import CudaContext, DeviceBuffer, Event, Graph, load, synth
+    from inferrous_amd import _lib
+    ctx = CudaContext(0)
+    mod = load(ctx)
+    s = ctx.new_stream()
+    L = _lib.lib()
+    nl, tick_us = 36, 0.01
+    shapes = [(129, si) for si in range(4)] + [(16, 3), (64, 3), (16, 2)]
+    print(f"{'shape':14s} {'M':>4s} {'WGs':>4s} {'split':>5s} {'prologue':>13s} {'stream':>13s} {'end':>6s} "
+          f"{'between':>7s} {'period':>6s} {'plain us':>8s} {'pull us':>7s} {'HBM us':>6s}   "
+          f"(us, medians of launches 2..35; med/last wave)", flush=True)
+    for m, si in shapes:
+        name, n, k = synth.DECODE_SHAPES[si]
+        mats = []
+        for layer in range(nl):
+            w = DeviceBuffer.zeroed(s, n * k, np.int8)
+            ws = DeviceBuffer.zeroed(s, n, np.float32)
+            mod.synth_i8(s, w, SEED_W, synth.weight_stream(layer, si))
+            mod.synth_f32(s, ws, SEED_S, synth.scale_stream(layer, si), 1e-3, 1e-2)
+            mats.append((w, ws))
+        x = synth.student_t_rows(700 + si, m, k)
+        q, sc = DeviceBuffer.zeroed(s, m * k, np.int8), DeviceBuffer.zeroed(s, m, np.float32)
+        mod.quantize(s, None, DeviceBuffer.from_host(s, x.reshape(-1)), k, q, sc)
+        out = DeviceBuffer.zeroed(s, m * n, np.uint16)
+        wsb = int(L.w8a8_linear_workspace_bytes(m, n, k))
+        work = DeviceBuffer.zeroed(s, max(wsb, 16), np.uint8)
+        need = int(L.w8a8_diag_gemm_timeline_stamps(m, n, k, wsb))
+        if need == 0:
+            print(f"{name:14s} {m:4d}: not a gemm_tall route", flush=True)
+            continue
+        stamps = DeviceBuffer.zeroed(s, nl * need, np.uint64)
+        route = np.zeros(20, np.int32)
+        _lib.check(L.w8a8_diag_linear_route(m, n, k, _lib.OUT_BF16, 0, 0, wsb, route.ctypes.data, 20), "route")
+        wgs, splits, bn, ma = int(route[1]), int(route[14]), int(route[5]), int(route[10])
+
+        def launches():
+            for i, (w, ws) in enumerate(mats):
+                _lib.check(L.w8a8_diag_gemm_timeline(s.handle, q.ptr, sc.ptr, m, w.ptr, ws.ptr, n, k, out.ptr,
+                                                     work.ptr, wsb, stamps.ptr + i * need * 8, need),
+                           "diag_gemm_timeline")
+
+        def plain():
+            for (w, ws) in mats:
+                mod.linear(s, None, q, sc, w, ws, k, out)
+        launches()
+        s.synchronize()
+        g = Graph(s)
+        with g:
+            launches()
+        for _ in range(20):
+            g.launch()
+        s.synchronize()
+        t = stamps.to_host_vec(s).astype(np.int64).reshape(nl, need // 4, 4)
+        start, end = t[:, :, 0].min(1), t[:, :, 3].max(1)
+        rel = (t - start[:, None, None]) * tick_us
+        med = lambda a: float(np.median(a))
+        pro_m, pro_x = med(np.median(rel[:, :, 1], 1)[2:]), med(rel[:, :, 1].max(1)[2:])
+        st_m, st_x = med(np.median(rel[:, :, 2], 1)[2:]), med(rel[:, :, 2].max(1)[2:])
+        e = med(rel[:, :, 3].max(1)[2:])
+        between = med(((start[1:] - end[:-1]) * tick_us)[1:])
+        period = med(((end[1:] - end[:-1]) * tick_us)[1:])
+        plain()  # eager first: reserves the stream's split-K workspace outside capture
+        s.synchronize()
+        pg = Graph(s)
+        with pg:
+            plain()
+        for _ in range(5):
+            pg.launch()
+        s.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        for _ in range(20):
+            pg.launch()
+        e1.record(s)
+        e1.synchronize()
+        plain_us = e0.elapsed_ms(e1) * 1e3 / 20 / nl
+        rows = -(-m // 8) * 8
+        pull = wgs * (rows + bn) * (k // splits)            # bytes pulled L2 -> CU
+        pull_us = (pull / wgs) / 30.0 / 2.1e3                 # 30 B/clk at 2.1 GHz, per CU
+        hbm_us = (n * k + m * k) / 8e12 * 1e6
+        print(f"{name:14s} {m:4d} {wgs:4d} {splits:5d} {pro_m:6.2f}/{pro_x:6.2f} {st_m:6.2f}/{st_x:6.2f} {e:6.2f} "
+              f"{between:7.2f} {period:6.2f} {plain_us:8.2f} {pull_us:7.2f} {hbm_us:6.2f}", flush=True)
+        del mats, stamps, g, pg
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -382,6 +485,8 @@ def main() -> int:
                     help="run only the ragged small-batch workload for a kernel-trace profile")
     ap.add_argument("--timeline", action="store_true",
                     help="run only the per-wave clock timeline of the decode GEMV launches")
+    ap.add_argument("--gemm-timeline", action="store_true",
+                    help="run only the per-wave clock timeline of gemm_tall at M = 129 and the ragged batches")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this W8A8 path has no multi-GPU mode "
@@ -399,6 +504,8 @@ def main() -> int:
         return ragged_profile_run()
     if args.timeline:
         return timeline_run()
+    if args.gemm_timeline:
+        return gemm_timeline_run()
     if args.chain_profile:
         return chain_profile_run()
 

@@ -36,6 +36,28 @@ int w8a8_diag_linear_timeline(void *stream, const int8_t *q, const float *asc,
                               uint32_t k, void *out, int out_dtype,
                               uint64_t *stamps, size_t stamps_len);
 
+/* Number of uint64 stamps w8a8_diag_gemm_timeline writes for an (m, n, k)
+ * projection given workspace_bytes of split-K workspace: 4 per wave of the
+ * gemm_tall launch; 0 when the route is not gemm_tall (M > 256, K % 128 != 0,
+ * or a small-M shape the skinny kernel takes). */
+size_t w8a8_diag_gemm_timeline_stamps(size_t m, size_t n, uint32_t k,
+                                      size_t workspace_bytes);
+
+/* w8a8_linear_ex with BF16 outputs (out: m x n) on its gemm_tall route, run
+ * by the same kernel with the same launch (and, for a split-K route, the same
+ * slab epilogue launch after it), timed: out gets the same values as
+ * w8a8_linear_ex, and wave w of workgroup b writes the device's 100 MHz clock
+ * (s_memrealtime) into stamps[4 (8 b + w) .. + 3]: at its start, once stage
+ * 0 of both rings has landed, after its last MFMA (or, for a wave that holds
+ * no rows, its last DMA) issue, and once its stores are acknowledged.
+ * W8A8_ESHAPE when the route is not gemm_tall; stamps_len at least
+ * w8a8_diag_gemm_timeline_stamps(m, n, k, workspace_bytes). */
+int w8a8_diag_gemm_timeline(void *stream, const int8_t *q, const float *asc,
+                            size_t m, const int8_t *w, const float *ws,
+                            size_t n, uint32_t k, void *out, void *workspace,
+                            size_t workspace_bytes, uint64_t *stamps,
+                            size_t stamps_len);
+
 /* ------------------------------------------------------------ launch routes
  * The kernel launch a call makes, decided on the host and returned as
  * W8A8_DIAG_ROUTE_LEN int32 values, so that host-side checks (the indexing

@@ -115,6 +115,8 @@ DIAG_SIGNATURES: dict[str, tuple] = {
     "w8a8_diag_linear_timeline_stamps": (S, [S, U32]),
     "w8a8_diag_linear_timeline": (I, [P, P, P, P, P, S, U32, P, I, P, S]),
     "w8a8_diag_linear_route": (I, [S, S, U32, I, I, I, S, P, S]),
+    "w8a8_diag_gemm_timeline_stamps": (S, [S, S, U32, S]),
+    "w8a8_diag_gemm_timeline": (I, [P, P, P, S, P, P, S, U32, P, P, S, P, S]),
     "w8a8_diag_argmax_route": (I, [S, U32, P, S]),
 }
 

@@ -944,6 +944,48 @@ int w8a8_diag_linear_timeline(void* stream, const int8_t* q, const float* asc, c
                                          stamps));
 }
 
+static GemmArgs timeline_args(const int8_t* q, const float* asc, size_t m, const int8_t* w, const float* ws,
+                               size_t n, uint32_t k, void* out, void* workspace, size_t workspace_bytes) {
+  GemmArgs g{};
+  g.q = q;
+  g.asc = asc;
+  g.m = (uint32_t)m;
+  g.w = w;
+  g.ws = ws;
+  g.n = (uint32_t)n;
+  g.k = k;
+  g.out = out;
+  g.out_dtype = W8A8_OUT_BF16;
+  g.partials = static_cast<int32_t*>(workspace);
+  g.partial_bytes = workspace ? workspace_bytes : 0;
+  return g;
+}
+
+size_t w8a8_diag_gemm_timeline_stamps(size_t m, size_t n, uint32_t k, size_t workspace_bytes) {
+  if (m == 0 || n == 0 || m > kU32Max || n > kU32Max || k == 0 || k % 16 != 0) return 0;
+  static const float kDummy[4] = {0.f, 0.f, 0.f, 0.f};
+  GemmArgs g = timeline_args(nullptr, nullptr, m, nullptr, nullptr, n, k, nullptr,
+                             workspace_bytes ? (void*)kDummy : nullptr, workspace_bytes);
+  return 4 * gemm_timeline_waves(g);
+}
+
+int w8a8_diag_gemm_timeline(void* stream, const int8_t* q, const float* asc, size_t m, const int8_t* w,
+                            const float* ws, size_t n, uint32_t k, void* out, void* workspace,
+                            size_t workspace_bytes, uint64_t* stamps, size_t stamps_len) {
+  const int c = check_linear(q, asc, m, w, ws, n, k, out, W8A8_OUT_BF16);
+  if (c != W8A8_OK) return c;
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (workspace && !al(workspace, 16)) return W8A8_EALIGN;
+  const size_t need = w8a8_diag_gemm_timeline_stamps(m, n, k, workspace ? workspace_bytes : 0);
+  if (need == 0) return W8A8_ESHAPE;  // not a gemm_tall route
+  if (!stamps) return W8A8_ENULL;
+  if (!al(stamps, 8)) return W8A8_EALIGN;
+  if (stamps_len < need) return W8A8_EWORKSPACE;
+  if (!ready()) return W8A8_EINIT;
+  const GemmArgs g = timeline_args(q, asc, m, w, ws, n, k, out, workspace, workspace_bytes);
+  return hip_status(launch_gemm_timeline((hipStream_t)stream, g, stamps));
+}
+
 // Fixed layout of a route record (include/inferrous_w8a8_diag.h).
 static void put_route(int32_t* r, int family, uint32_t gx, uint32_t gy, uint32_t block) {
   for (size_t i = 0; i < W8A8_DIAG_ROUTE_LEN; ++i) r[i] = 0;

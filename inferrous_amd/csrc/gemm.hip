@@ -616,8 +616,15 @@ __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
 // and counts its waits with its own na, nb.  During stage kt it issues
 // A(kt + SA - 1), then B(kt + SB - 1).
 // Split-K as in gemm_dma: workgroup (tile, split) writes i32 slab `split`.
-template <int BN, int SA, int SB, int MA, int EP, bool ROT = false>
-__global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, uint32_t splits) {
+// TIMED (diagnostics only, w8a8_diag_gemm_timeline): every wave also
+// records the 100 MHz device clock at its start, once stage 0 has landed
+// (the prologue), after its last MFMA / DMA issue, and once its stores are
+// acknowledged, into stamps[4 g .. 4 g + 3] (g = workgroup * 8 + wave).
+template <int BN, int SA, int SB, int MA, int EP, bool ROT = false, bool TIMED = false>
+__global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, uint32_t splits,
+                                                 uint64_t* stamps) {
+  uint64_t ts[4] = {0, 0, 0, 0};
+  if constexpr (TIMED) ts[0] = __builtin_amdgcn_s_memrealtime();
   constexpr int FN = BN / 32;
   constexpr int ASL = MA * 128, BSL = BN * 128;
   constexpr uint32_t NB = BN / 8;
@@ -748,6 +755,10 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
   if (KT >= (uint32_t)SB - 1) wait_vmcnt_dyn((SA - 2) * na + (SB - 2) * nb);
   else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
+  if constexpr (TIMED) ts[1] = __builtin_amdgcn_s_memrealtime();
+  auto stamp_stream_end = [&]() {
+    if constexpr (TIMED) ts[2] = __builtin_amdgcn_s_memrealtime();
+  };
 
   if constexpr (MA == 64) {
     // one 32 x 32 block per wave: block `wave` of the (M / 32) x FN grid
@@ -766,10 +777,12 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
                  f.b = *(const v4i*)(bb + (kt % SB) * BSL + off[i]);
                },
                [&](const Frag& f) { acc = mfma32(f.a, f.b, acc); });
+      stamp_stream_end();
       const v16i blocks[1][1] = {{acc}};
       store_blocks<EP, 1, 1>(a, blocks, 32 * mb, n0 + 32 * nbk, lane);
     } else {
       move_only();
+      stamp_stream_end();
     }
   } else {
     if (32u * wave < a.m) {
@@ -789,10 +802,21 @@ __global__ __launch_bounds__(512) void gemm_tall(GemmArgs a, uint32_t tiles_n, u
 #pragma unroll
                  for (int j = 0; j < FN; ++j) acc[j] = mfma32(f.a, f.b[j], acc[j]);
                });
+      stamp_stream_end();
       const v16i (&blocks)[1][FN] = *reinterpret_cast<const v16i(*)[1][FN]>(&acc);
       store_blocks<EP, 1, FN>(a, blocks, 32 * wave, n0, lane);
     } else {
       move_only();
+      stamp_stream_end();
+    }
+  }
+  if constexpr (TIMED) {
+    __builtin_amdgcn_s_waitcnt(0);
+    ts[3] = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) {
+      uint64_t* o = stamps + ((size_t)blockIdx.x * 8 + wave) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = ts[i];
     }
   }
 }
@@ -1094,18 +1118,34 @@ static hipError_t launch_tall(hipStream_t st, const GemmArgs& a, uint32_t splits
   const dim3 grid(tn * splits), block(512);
   if (splits > 1)
     return launch_slabs(st, a, splits, stream_slabs(a, splits), [&](auto ep, const GemmArgs& p) {
-      hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, decltype(ep)::value, false>), grid, block, 0, st, p, tn, splits);
+      hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, decltype(ep)::value, false>), grid, block, 0, st, p, tn, splits,
+                         nullptr);
     });
   if (a.out_dtype == W8A8_OUT_I32)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32, kRotateK>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_I32, kRotateK>), grid, block, 0, st, a, tn, 1u, nullptr);
   else if (a.out_dtype == W8A8_OUT_F32 && a.residual)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32_RES, kRotateK>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32_RES, kRotateK>), grid, block, 0, st, a, tn, 1u, nullptr);
   else if (a.out_dtype == W8A8_OUT_F32)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32, kRotateK>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_F32, kRotateK>), grid, block, 0, st, a, tn, 1u, nullptr);
   else if (a.residual)
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16_RES, kRotateK>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16_RES, kRotateK>), grid, block, 0, st, a, tn, 1u, nullptr);
   else
-    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16, kRotateK>), grid, block, 0, st, a, tn, 1u);
+    hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16, kRotateK>), grid, block, 0, st, a, tn, 1u, nullptr);
+  return hipGetLastError();
+}
+
+// Diagnostics: gemm_tall with the per-wave clock stamps (TIMED), BF16
+// outputs without a residual; the split-K epilogue follows as in launch_tall.
+template <int BN, int SA, int SB, int MA>
+static hipError_t launch_tall_timed(hipStream_t st, const GemmArgs& a, uint32_t splits, uint64_t* stamps) {
+  const uint32_t tn = (a.n + BN - 1) / BN;
+  const dim3 grid(tn * splits), block(512);
+  if (splits > 1)
+    return launch_slabs(st, a, splits, stream_slabs(a, splits), [&](auto ep, const GemmArgs& p) {
+      hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, decltype(ep)::value, false, true>), grid, block, 0, st, p, tn,
+                         splits, stamps);
+    });
+  hipLaunchKernelGGL((gemm_tall<BN, SA, SB, MA, EP_BF16, kRotateK, true>), grid, block, 0, st, a, tn, 1u, stamps);
   return hipGetLastError();
 }
 
@@ -1198,6 +1238,26 @@ GemmRoute gemm_route(const GemmArgs& a) {
   r.grid_x = (a.m + r.bm - 1) / r.bm * ((a.n + r.bn - 1) / r.bn);
   r.block = 256;
   return r;
+}
+
+size_t gemm_timeline_waves(const GemmArgs& a) {
+  const GemmRoute r = gemm_route(a);
+  return r.family == kRouteTall ? (size_t)r.grid_x * 8 : 0;
+}
+
+hipError_t launch_gemm_timeline(hipStream_t st, const GemmArgs& a, uint64_t* stamps) {
+  const GemmRoute r = gemm_route(a);
+  if (r.family != kRouteTall || a.out_dtype != W8A8_OUT_BF16 || a.residual) return hipErrorInvalidValue;
+  if (r.ma == 64)
+    return r.bn == 96 ? launch_tall_timed<96, 4, 4, 64>(st, a, r.splits, stamps)
+                      : launch_tall_timed<64, 4, 4, 64>(st, a, r.splits, stamps);
+  if (r.ma == 160)
+    return r.bn == 96 ? launch_tall_timed<96, 4, 4, 160>(st, a, r.splits, stamps)
+                      : launch_tall_timed<64, 4, 4, 160>(st, a, r.splits, stamps);
+  if (r.bn == 96)
+    return r.splits > 1 ? launch_tall_timed<96, 3, 3, 256>(st, a, r.splits, stamps)
+                        : launch_tall_timed<96, 2, 4, 256>(st, a, r.splits, stamps);
+  return launch_tall_timed<64, 4, 4, 256>(st, a, r.splits, stamps);
 }
 
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {

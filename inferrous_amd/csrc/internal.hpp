@@ -86,6 +86,9 @@ struct GemmRoute {
   uint32_t grid_x, grid_y, block;   // the GEMM launch
 };
 GemmRoute gemm_route(const GemmArgs& a);
+// Diagnostics: the gemm_tall route with per-wave clock stamps (4 per wave).
+size_t gemm_timeline_waves(const GemmArgs& a);
+hipError_t launch_gemm_timeline(hipStream_t st, const GemmArgs& a, uint64_t* stamps);
 
 // The launch a GEMV call makes (launch_gemv / launch_gemv_argmax): family
 // kRouteGemvM1One, kRouteGemvM1 or kRouteGemvMt; `rows` rows per row group

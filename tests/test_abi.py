@@ -10,6 +10,7 @@ import subprocess
 import sys
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from inferrous_amd import _lib
@@ -107,6 +108,22 @@ def test_diag_timeline_stamp_count():
     assert L.w8a8_diag_linear_timeline_stamps(1, 4096) == 3 * 4
     assert L.w8a8_diag_linear_timeline_stamps(4096, 1024) == 0
     assert L.w8a8_diag_linear_timeline_stamps(0, 4096) == 0
+
+
+def test_diag_gemm_timeline_stamp_count():
+    """Four stamps per wave of the gemm_tall launch (8 waves per workgroup,
+    the route's grid); 0 where the route is not gemm_tall."""
+    L = _lib.lib()
+    route = np.zeros(20, np.int32)
+    for (m, n, k) in [(129, 4096, 4096), (129, 24576, 4096), (16, 4096, 12288), (200, 6100, 4096)]:
+        wsb = L.w8a8_linear_workspace_bytes(m, n, k)
+        assert L.w8a8_diag_linear_route(m, n, k, _lib.OUT_BF16, 0, 0, wsb, route.ctypes.data, 20) == 0
+        assert route[0] == 12
+        assert L.w8a8_diag_gemm_timeline_stamps(m, n, k, wsb) == 4 * 8 * route[1]
+    assert L.w8a8_diag_gemm_timeline_stamps(512, 4096, 4096, 0) == 0      # gemm_dma
+    assert L.w8a8_diag_gemm_timeline_stamps(3, 4096, 4096, 0) == 0        # gemm_skinny
+    assert L.w8a8_diag_gemm_timeline_stamps(129, 4096, 4100, 0) == 0      # K % 16 != 0
+    assert L.w8a8_diag_gemm_timeline_stamps(0, 4096, 4096, 0) == 0
 
 
 @pytest.mark.skipif(no_device_status() > 0, reason="validation-order test assumes no GPU")

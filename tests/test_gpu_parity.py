@@ -280,6 +280,35 @@ def test_decode_gemv_one_matrix_routes(env, k, n):
             check(bc, (bits(comb) >> 16).astype(np.uint16), "residual combined bf16")
 
 
+@pytest.mark.parametrize("m,n,k", [(129, 4096, 4096), (129, 24576, 4096), (16, 4096, 12288), (200, 6100, 4096),
+                                   (64, 4096, 12288)])
+def test_diag_gemm_timeline_matches_linear(env, m, n, k):
+    """The timed gemm_tall route (w8a8_diag_gemm_timeline) writes the BF16
+    values w8a8_linear writes with the same workspace -- split-K routes
+    included -- and four ordered stamps per wave."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    L = _lib.lib()
+    rng = np.random.default_rng(9400 + m + n)
+    q = dev(s, rng.integers(-127, 128, size=(m, k), dtype=np.int8))
+    w = dev(s, rng.integers(-127, 128, size=(n, k), dtype=np.int8))
+    asc = dev(s, (rng.random(m) / 64 + 1e-4).astype(F32))
+    ws = dev(s, (rng.random(n) / 64 + 1e-4).astype(F32))
+    wsb = int(L.w8a8_linear_workspace_bytes(m, n, k))
+    work = DeviceBuffer.zeroed(s, max(wsb, 16), np.uint8)
+    need = int(L.w8a8_diag_gemm_timeline_stamps(m, n, k, wsb))
+    assert need > 0 and need % 32 == 0
+    stamps = DeviceBuffer.zeroed(s, need, np.uint64)
+    got = DeviceBuffer.zeroed(s, m * n, np.uint16)
+    _lib.check(L.w8a8_diag_gemm_timeline(s.handle, q.ptr, asc.ptr, m, w.ptr, ws.ptr, n, k, got.ptr, work.ptr, wsb,
+                                         stamps.ptr, need), "diag_gemm_timeline")
+    want = DeviceBuffer.zeroed(s, m * n, np.uint16)
+    mod.linear(s, None, q, asc, w, ws, k, want)
+    assert np.array_equal(got.to_host_vec(s), want.to_host_vec(s))
+    t = stamps.to_host_vec(s).astype(np.int64).reshape(-1, 4)
+    assert (t > 0).all() and (np.diff(t, axis=1) >= 0).all()
+
+
 @pytest.mark.parametrize("k,n", [(4096, 6144), (4096, 8193), (12288, 4097)])
 def test_diag_timeline_matches_linear(env, k, n):
     """The timed diagnostics GEMV writes the values w8a8_linear writes, and
