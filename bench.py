@@ -365,7 +365,7 @@ def timeline_run() -> int:
 
 def gemm_timeline_run() -> int:
     """Where a gemm_tall launch spends its time (M = 129 on the four layer
-    shapes, the ragged M = 16 / 64 down and M = 16 gate_up), without a
+    shapes, the ragged M = 24 / 64 down and M = 16 gate_up), without a
     profiler.  For each shape, 36 distinct-weight launches of
     w8a8_diag_gemm_timeline (the kernel and launch of w8a8_linear_ex's
     gemm_tall route with per-wave stamps of the 100 MHz clock, and the same
@@ -387,7 +387,7 @@ def gemm_timeline_run() -> int:
     s = ctx.new_stream()
     L = _lib.lib()
     nl, tick_us = 36, 0.01
-    shapes = [(129, si) for si in range(4)] + [(16, 3), (64, 3), (16, 2)]
+    shapes = [(129, si) for si in range(4)] + [(24, 3), (64, 3), (16, 2)]
     print(f"{'shape':14s} {'M':>4s} {'WGs':>4s} {'split':>5s} {'prologue':>13s} {'stream':>13s} {'end':>6s} "
           f"{'between':>7s} {'period':>6s} {'plain us':>8s} {'pull us':>7s} {'HBM us':>6s}   "
           f"(us, medians of launches 2..35; med/last wave)", flush=True)

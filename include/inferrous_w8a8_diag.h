@@ -39,7 +39,7 @@ int w8a8_diag_linear_timeline(void *stream, const int8_t *q, const float *asc,
 /* Number of uint64 stamps w8a8_diag_gemm_timeline writes for an (m, n, k)
  * projection given workspace_bytes of split-K workspace: 4 per wave of the
  * gemm_tall launch; 0 when the route is not gemm_tall (M > 256, K % 128 != 0,
- * or a small-M shape the skinny kernel takes). */
+ * or a small-M shape the narrow or skinny kernel takes). */
 size_t w8a8_diag_gemm_timeline_stamps(size_t m, size_t n, uint32_t k,
                                       size_t workspace_bytes);
 
@@ -65,11 +65,13 @@ int w8a8_diag_gemm_timeline(void *stream, const int8_t *q, const float *asc,
  * arithmetic over exactly the grid the library launches.  Nothing runs on a
  * device; no device is needed.
  *   [0] family: 0 none (m or n is 0), 1 gemv_m1_one, 2 gemv_m1, 3 gemv_mt,
- *       11 gemm_skinny, 12 gemm_tall, 13 gemm_dma, 14 gemm_tiled
+ *       11 gemm_skinny, 12 gemm_tall, 13 gemm_dma, 14 gemm_tiled, 15 gemm_narrow
  *   [1] grid x  [2] grid y  [3] threads per workgroup
- *   [4] BM  [5] BN  [6] WM  [7] WN  [8] SA  [9] SB  [10] MA (gemm_tall's M tile)
- *   [11] MT (skinny: 16-row tiles; gemv_mt: activation rows per pass)
- *   [12] S (skinny waves)  [13] U (unroll)  [14] split-K slabs (1: none)
+ *   [4] BM  [5] BN  [6] WM  [7] WN  [8] SA (gemm_narrow: ring stages)  [9] SB
+ *   [10] MA (gemm_tall's M tile)
+ *   [11] MT (skinny, narrow: 16-row tiles; gemv_mt: activation rows per pass)
+ *   [12] S (skinny, narrow: waves)  [13] U (skinny: unroll; narrow: live
+ *        activation DMA loads per stage)  [14] split-K slabs (1: none)
  *   [15] slabs streamed  [16] split-K epilogue columns per thread (4 or 8)
  *   [17] GEMV rows per wave  [18] GEMV K / 1024  [19] GEMV waves per workgroup
  * Unused fields are 0. */

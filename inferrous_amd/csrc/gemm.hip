@@ -37,6 +37,15 @@
 //    one each (M <= 64) or 32-row slices of all BN columns, and those
 //    holding none only move data; activation rows past M are never loaded;
 //    split-K on narrow n.
+//  * gemm_narrow (M <= 16, or M <= 32 on n <= 4096 at k <= 4096, where the
+//    n / 96 tiles are fewer than 224 and k splits into S slices of 128-byte
+//    stages): one workgroup owns 16 weight rows; its S waves split K into S
+//    slices, and each wave streams its slice through its own global -> LDS
+//    ring (16 weight rows and the live activation rows of a 128-byte stage,
+//    global_load_lds_dwordx4: eight whole lines per instruction), so the K
+//    loop has no workgroup barrier and no split-K slabs leave the CU.  The S
+//    partial 16 x 16 tiles are summed through LDS (exact) and stored by the
+//    fused epilogue.
 //  * gemm_skinny (small M on narrow n, HBM-bound, 16x16x64 MFMA): one
 //    workgroup owns 16 weight rows; its S waves split K and stream their
 //    weight fragments straight from HBM into MFMA B operands (no LDS round
@@ -255,6 +264,112 @@ __device__ __forceinline__ void wait_vmcnt() {
 // that is streamed: non-temporal stores, read back once by the slab epilogue.
 enum { EP_I32 = 0, EP_F32 = 1, EP_BF16 = 2, EP_F32_RES = 3, EP_BF16_RES = 4, EP_SLAB = 5 };
 constexpr bool raw_i32(int ep) { return ep == EP_I32 || ep == EP_SLAB; }
+
+// ---------------------------------------------------------------- narrow
+// Workgroup b owns output columns [16 b, 16 b + 16) and all M rows (MB
+// 16-row blocks).  Wave w sums the K slice [w K / S, (w + 1) K / S) in
+// 128-byte stages (the host guarantees K % (128 S) == 0) through its own
+// ring of R stages: a stage holds 16 weight rows, then 16 MB activation
+// rows, 128 bytes each; DMA instruction j fills rows 8j .. 8j + 7, lane l
+// chunk l % 8 of row 8j + l / 8 with global chunk (l % 8) ^ (row % 8), so
+// that the 16-row fragment reads (lane l: row l % 16) meet eight distinct
+// bank groups.  Only the first LAL activation instructions are issued (the
+// host picks LAL = ceil(M / 8)); lanes of rows >= M load nothing, so those
+// LDS rows hold stale bytes whose products reach only accumulator rows >= M,
+// which are never stored.  Weight rows past N re-read row N - 1.  A wave
+// reads only its own ring, so the K loop needs no workgroup barrier: each
+// stage is waited for with vmcnt (every issued instruction has a live lane,
+// so the count is exact), and a slot is refilled only after the previous
+// stage's fragment reads have returned.
+template <int MB, int LAL, int S, int R>
+__global__ __launch_bounds__(64 * S) void gemm_narrow(GemmArgs a) {
+  constexpr int ROWS = 16 * (1 + MB);
+  constexpr int STAGE = ROWS * 128;
+  constexpr int L = 2 + LAL;  // DMA instructions per stage
+  constexpr int RING = R * STAGE;
+  static_assert(MB >= 1 && LAL >= 1 && LAL <= 2 * MB, "live activation loads");
+  static_assert(R >= 2 && (R - 1) * L < 64, "ring depth");
+  static_assert(S * RING <= 160 * 1024, "LDS");
+  static_assert(S * MB * 4 * 64 * (int)sizeof(int) <= S * RING, "the reduction reuses the rings");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * RING];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const uint32_t n0 = blockIdx.x * 16, K = a.k, M = a.m, N = a.n;
+  const uint32_t KS = K / S, ST = KS / 128;
+  const size_t k0 = (size_t)wave * KS;
+  int8_t* const ring = lds + wave * RING;
+
+  const int8_t* src[L];
+  bool live[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const size_t chunk = (size_t)(((lane & 7) ^ (row & 7)) * 16);
+    if (row < 16) {
+      const uint32_t g = n0 + row;
+      src[j] = a.w + (size_t)(g < N ? g : N - 1) * K + k0 + chunk;
+      live[j] = true;
+    } else {
+      const uint32_t g = (uint32_t)(row - 16);
+      live[j] = g < M;
+      src[j] = a.q + (size_t)(live[j] ? g : 0) * K + k0 + chunk;
+    }
+  }
+  auto load = [&](uint32_t s) {
+    int8_t* const base = ring + (s % R) * STAGE;
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+      if (live[j])
+        __builtin_amdgcn_global_load_lds((const void*)(src[j] + (size_t)s * 128),
+                                         W8A8_LDS_PTR(base + j * 1024 + lane * 16), 16, 0, 0);
+  };
+
+  const int fr = lane & 15, fq = lane >> 4;
+  v4i acc[MB];
+#pragma unroll
+  for (int t = 0; t < MB; ++t) acc[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < R - 1; ++s)
+    if ((uint32_t)s < ST) load(s);
+  for (uint32_t s = 0; s < ST; ++s) {
+    if (s + R - 1 < ST) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // stage s - 1's fragment reads returned
+      load(s + R - 1);                                     // into stage s - 1's slot
+      wait_vmcnt<(R - 1) * L>();                           // stage s landed
+    } else {
+      wait_vmcnt<0>();
+    }
+    const int8_t* const base = ring + (s % R) * STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // the stage's two 64-byte k steps
+      const int c = 4 * h + fq;
+      const v4i b = *(const v4i*)(base + fr * 128 + ((c ^ (fr & 7)) * 16));
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        const int row = 16 + 16 * t + fr;
+        const v4i av = *(const v4i*)(base + row * 128 + ((c ^ (row & 7)) * 16));
+        acc[t] = mfma16(av, b, acc[t]);
+      }
+    }
+  }
+  __syncthreads();  // every wave is done with its ring
+  int* const red = reinterpret_cast<int*>(lds);
+#pragma unroll
+  for (int t = 0; t < MB; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[((wave * MB + t) * 4 + v) * 64 + lane] = acc[t][v];
+  __syncthreads();
+  // value v of lane l of block t: row 16 t + 4 (l / 16) + v, column n0 + l % 16
+  for (int i = threadIdx.x; i < MB * 4 * 64; i += 64 * S) {
+    const int l = i & 63, v = (i >> 6) & 3, t = i >> 8;
+    int sum = 0;
+#pragma unroll
+    for (int w = 0; w < S; ++w) sum += red[((w * MB + t) * 4 + v) * 64 + l];
+    const uint32_t r = 16 * t + 4 * (l >> 4) + v;
+    const uint32_t c = n0 + (l & 15);
+    if (r < M && c < N) epilogue_store(a, r, c, sum);
+  }
+}
 
 // Epilogue of a wave's FM x FN grid of 32x32 accumulator blocks whose top
 // left corner is (row0, col0).  Lane l, value v of block (i, j) is row
@@ -1000,6 +1115,34 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
 // 9.1 / 9.3, so it takes this plan from m = 8, o from m = 24.
 // Returns false when no plan applies (the gemm_dma or gemm_skinny routes
 // then run).  ma: the M tile (64, 160 or 256 rows).
+// gemm_narrow's plan: S = 4 waves below K = 8192 and 8 from there (each wave
+// keeps eight or more 128-byte stages), R-deep rings, MB 16-row blocks, LAL
+// = ceil(M / 8) activation DMA loads per stage.  It takes M <= 16 on the
+// narrow shapes, and M <= 32 where one workgroup per 16 columns fits the
+// CUs once at K <= 4096; the wide shapes (n / 96 >= 224 tiles) keep
+// gemm_tall's unsplit 96-column tiles.  Measured on MI355X, graphs of 36
+// distinct-weight launches, random operands, against the routes it
+// replaced (gemm_tall split-K 4 with its slab epilogue launch, gemm_skinny),
+// bit-identical outputs: down 4096 x 12288 at M = 2 / 4 / 8 / 12 / 16
+// 10.98 / 11.06 / 11.23 / 11.68 / 12.25 us against 12.64 / 12.72 / 12.77 /
+// 13.17 / 13.17 (S = 8); o 4096 x 4096 at M = 2 / 8 / 16 / 24 / 32 5.53 /
+// 5.63 / 5.73 / 6.63 / 7.01 against 6.94 / 7.46 / 7.84 / 8.36 / 8.77 (S = 4);
+// qkv 6144 x 4096 at M = 2 / 8 / 16 6.98 / 7.48 / 8.09 against 8.30 / 8.98 /
+// 9.25 (S = 4; 8.50 / 9.17 / 9.59 with S = 8).  At M = 24 and 32 down and
+// qkv are level or slower than gemm_tall (down 13.78 / 15.12 against 13.59 /
+// 14.03) and keep it.  Deeper rings (5) and 16 waves measured level or
+// slower.
+static bool narrow_plan(uint32_t m, uint32_t n, uint32_t k, int& S, int& R, int& MB, int& LAL) {
+  if (m == 0 || m > 32 || (n + 95) / 96 >= 224) return false;
+  S = k >= 8192 ? 8 : 4;
+  if (k % (128u * S) != 0) return false;
+  if (m > 16 && !(k <= 4096 && (n + 15) / 16 <= 256)) return false;
+  MB = m <= 16 ? 1 : 2;  // two blocks only at S = 4 (K <= 4096)
+  LAL = (int)((m + 7) / 8);
+  R = 4;
+  return true;
+}
+
 static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits, int& ma) {
   if (m == 0 || m > 256 || k % 128 != 0) return false;
   ma = m <= 64 ? 64 : m <= 160 ? 160 : 256;
@@ -1021,6 +1164,10 @@ size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
   int tile;
   uint32_t splits;
   int ma;
+  {
+    int S, R, MB, LAL;
+    if (narrow_plan(m, n, k, S, R, MB, LAL)) return 0;
+  }
   if (tall_plan(m, n, k, tile, splits, ma)) return splits > 1 ? (size_t)splits * m * n * sizeof(int32_t) : 0;
   if (!split_plan(m, n, k, splits)) return 0;
   return (size_t)splits * m * n * sizeof(int32_t);
@@ -1158,6 +1305,19 @@ GemmRoute gemm_route(const GemmArgs& a) {
   r.grid_y = 1;
   r.block = 512;
   if (a.m == 0 || a.n == 0) return r;
+  {
+    int S, R, MB, LAL;
+    if (narrow_plan(a.m, a.n, a.k, S, R, MB, LAL)) {
+      r.family = kRouteNarrow;
+      r.mt = MB;
+      r.s = S;
+      r.u = LAL;
+      r.sa = R;
+      r.grid_x = (a.n + 15) / 16;
+      r.block = 64 * S;
+      return r;
+    }
+  }
   // m <= 256 goes to gemm_tall when its plan applies.
   // Otherwise, for small m: from m = 8 the 8-wave kernel with 64-row tiles
   // streams the weights faster when n gives at least 128 tiles; below that
@@ -1260,6 +1420,32 @@ hipError_t launch_gemm_timeline(hipStream_t st, const GemmArgs& a, uint64_t* sta
   return launch_tall_timed<64, 4, 4, 256>(st, a, r.splits, stamps);
 }
 
+template <int MB, int LAL, int S, int R>
+static hipError_t launch_narrow_as(hipStream_t st, const GemmArgs& a, uint32_t grid) {
+  hipLaunchKernelGGL((gemm_narrow<MB, LAL, S, R>), dim3(grid), dim3(64 * S), 0, st, a);
+  return hipGetLastError();
+}
+
+// The instantiations narrow_plan can ask for: S = 4 with one or two 16-row
+// blocks, S = 8 (K >= 8192) with one; LAL = ceil(M / 8); R = 4.
+static hipError_t launch_narrow(hipStream_t st, const GemmArgs& a, const GemmRoute& r) {
+  const uint32_t g = r.grid_x;
+  if (r.s == 4) {
+    switch (r.u) {
+      case 1: return launch_narrow_as<1, 1, 4, 4>(st, a, g);
+      case 2: return launch_narrow_as<1, 2, 4, 4>(st, a, g);
+      case 3: return launch_narrow_as<2, 3, 4, 4>(st, a, g);
+      case 4: return launch_narrow_as<2, 4, 4, 4>(st, a, g);
+    }
+  } else if (r.s == 8) {
+    switch (r.u) {
+      case 1: return launch_narrow_as<1, 1, 8, 4>(st, a, g);
+      case 2: return launch_narrow_as<1, 2, 8, 4>(st, a, g);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
   const GemmRoute r = gemm_route(a);
   auto is = [&](int bm, int bn, int wm, int wn, int sa, int sb) {
@@ -1276,6 +1462,8 @@ hipError_t launch_gemm(hipStream_t st, const GemmArgs& a) {
       if (r.bn == 96)
         return r.splits > 1 ? launch_tall<96, 3, 3, 256>(st, a, r.splits) : launch_tall<96, 2, 4, 256>(st, a, r.splits);
       return launch_tall<64, 4, 4, 256>(st, a, r.splits);
+    case kRouteNarrow:
+      return launch_narrow(st, a, r);
     case kRouteSkinny:
       if (r.mt == 1) hipLaunchKernelGGL((gemm_skinny<1, 4, 4>), dim3(r.grid_x, 1), dim3(r.block), 0, st, a);
       else if (r.mt == 2) hipLaunchKernelGGL((gemm_skinny<2, 4, 4>), dim3(r.grid_x, 1), dim3(r.block), 0, st, a);

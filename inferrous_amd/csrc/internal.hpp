@@ -75,11 +75,13 @@ size_t gemm_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 // diagnostics export it so that host-side checks can replay each kernel's
 // index arithmetic over its grid.
 enum { kRouteNone = 0, kRouteGemvM1One = 1, kRouteGemvM1 = 2, kRouteGemvMt = 3, kRouteSkinny = 11,
-       kRouteTall = 12, kRouteDma = 13, kRouteTiled = 14 };
+       kRouteTall = 12, kRouteDma = 13, kRouteTiled = 14, kRouteNarrow = 15 };
 struct GemmRoute {
-  int family;                       // kRouteSkinny, kRouteTall, kRouteDma, kRouteTiled (kRouteNone: m or n is 0)
-  int bm, bn, wm, wn, sa, sb, ma;   // dma / tiled tile; tall: bn, sa, sb, ma
-  int mt, s, u;                     // skinny: 16-row tiles, waves, unroll
+  int family;                       // kRouteSkinny, kRouteTall, kRouteDma, kRouteTiled, kRouteNarrow
+                                    // (kRouteNone: m or n is 0)
+  int bm, bn, wm, wn, sa, sb, ma;   // dma / tiled tile; tall: bn, sa, sb, ma; narrow: sa = ring stages
+  int mt, s, u;                     // skinny: 16-row tiles, waves, unroll; narrow: 16-row tiles, waves,
+                                    // live activation DMA loads per stage
   uint32_t splits;                  // split-K slabs (1: none)
   int nt_slabs;                     // slabs streamed (EP_SLAB)
   int epi_cols;                     // split-K epilogue columns per thread (4 or 8)

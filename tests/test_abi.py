@@ -115,13 +115,15 @@ def test_diag_gemm_timeline_stamp_count():
     the route's grid); 0 where the route is not gemm_tall."""
     L = _lib.lib()
     route = np.zeros(20, np.int32)
-    for (m, n, k) in [(129, 4096, 4096), (129, 24576, 4096), (16, 4096, 12288), (200, 6100, 4096)]:
+    for (m, n, k) in [(129, 4096, 4096), (129, 24576, 4096), (24, 4096, 12288), (200, 6100, 4096)]:
         wsb = L.w8a8_linear_workspace_bytes(m, n, k)
         assert L.w8a8_diag_linear_route(m, n, k, _lib.OUT_BF16, 0, 0, wsb, route.ctypes.data, 20) == 0
         assert route[0] == 12
         assert L.w8a8_diag_gemm_timeline_stamps(m, n, k, wsb) == 4 * 8 * route[1]
     assert L.w8a8_diag_gemm_timeline_stamps(512, 4096, 4096, 0) == 0      # gemm_dma
-    assert L.w8a8_diag_gemm_timeline_stamps(3, 4096, 4096, 0) == 0        # gemm_skinny
+    assert L.w8a8_diag_gemm_timeline_stamps(3, 4096, 4096, 0) == 0        # gemm_narrow
+    assert L.w8a8_diag_gemm_timeline_stamps(16, 4096, 12288, 0) == 0      # gemm_narrow
+    assert L.w8a8_diag_gemm_timeline_stamps(3, 4096, 1040, 0) == 0        # gemm_skinny
     assert L.w8a8_diag_gemm_timeline_stamps(129, 4096, 4100, 0) == 0      # K % 16 != 0
     assert L.w8a8_diag_gemm_timeline_stamps(0, 4096, 4096, 0) == 0
 
@@ -361,9 +363,11 @@ def test_fused_and_workspace_entries_validation():
     assert nq(x=None) == _lib.ENULL and nq(maxima=None) == _lib.ENULL
     assert nq(out=A + 2) == _lib.EALIGN
     # linear_ex: the split-K workspace is optional, never required
-    # the MFMA family's split plan for down at m = 1 (4 slabs); AUTO runs dot4 there
-    assert L.w8a8_linear_workspace_bytes(1, 4096, 12288) == 4 * 1 * 4096 * 4
-    assert L.w8a8_linear_workspace_bytes(4, 4096, 4096) == 0       # skinny kernel: none
+    # the MFMA family's split plan for down at m = 24 (4 slabs); below m = 17 the narrow kernel needs none
+    assert L.w8a8_linear_workspace_bytes(24, 4096, 12288) == 4 * 24 * 4096 * 4
+    assert L.w8a8_linear_workspace_bytes(1, 4096, 12288) == 0      # narrow kernel: none
+    assert L.w8a8_linear_workspace_bytes(4, 4096, 4096) == 0       # narrow kernel: none
+    assert L.w8a8_linear_workspace_bytes(4, 4096, 1040) == 0       # skinny kernel: none
     assert L.w8a8_linear_workspace_bytes(512, 4096, 12288) > 0     # 128x128 split in two
     assert L.w8a8_linear_workspace_bytes(512, 4096, 12288) == 2 * 512 * 4096 * 4
     ex = lambda **kw: L.w8a8_linear_ex(  # noqa: E731
@@ -519,16 +523,18 @@ def test_noalloc_argmax_validation():
 
 def test_workspace_queries_by_route_and_batch_range():
     """The split-K workspace need depends on the route and is not monotone
-    in M: AUTO at M <= 2 runs the dot4 GEMV and needs nothing, DOT4 never
-    does, MFMA keeps the shape's need; the largest need over M = 1..512 for
-    qkv (6144 x 4096) sits at M = 256, where M = 512 needs none."""
+    in M: the narrow kernel (M <= 16 on down) needs none, the one-M-tile
+    split-K route above it does, AUTO at M <= 2 runs the dot4 GEMV, DOT4
+    never needs any, MFMA keeps the shape's need; the largest need over
+    M = 1..512 for qkv (6144 x 4096) sits at M = 256, where M = 512 needs
+    none."""
     L = _lib.lib()
     down = (4096, 12288)
-    assert L.w8a8_linear_workspace_bytes(1, *down) > 0
-    assert L.w8a8_linear_workspace_bytes_path(1, *down, _lib.PATH_AUTO) == 0
+    assert all(L.w8a8_linear_workspace_bytes(m, *down) == 0 for m in range(1, 17))
+    assert L.w8a8_linear_workspace_bytes(17, *down) > 0
+    assert L.w8a8_linear_workspace_bytes_path(24, *down, _lib.PATH_AUTO) == L.w8a8_linear_workspace_bytes(24, *down)
+    assert L.w8a8_linear_workspace_bytes_path(24, *down, _lib.PATH_MFMA) == L.w8a8_linear_workspace_bytes(24, *down)
     assert L.w8a8_linear_workspace_bytes_path(2, *down, _lib.PATH_AUTO) == 0
-    assert L.w8a8_linear_workspace_bytes_path(3, *down, _lib.PATH_AUTO) == L.w8a8_linear_workspace_bytes(3, *down)
-    assert L.w8a8_linear_workspace_bytes_path(1, *down, _lib.PATH_MFMA) == L.w8a8_linear_workspace_bytes(1, *down)
     assert L.w8a8_linear_workspace_bytes_path(64, *down, _lib.PATH_DOT4) == 0
     assert L.w8a8_linear_workspace_bytes_path(64, *down, 7) == 0
     qkv = (6144, 4096)

@@ -177,11 +177,11 @@ def test_linear_random_shapes(env, m):
             assert np.array_equal(ob.to_host_vec(s), outb), f"{op} bf16 m={m} n={n} k={k}"
 
 
-@pytest.mark.parametrize("m", [7, 8, 12, 23, 24])
+@pytest.mark.parametrize("m", [7, 8, 12, 16, 17, 23, 24, 32, 33])
 @pytest.mark.parametrize("n", [6144, 4096])
 def test_small_batch_qkv_o_routes(env, m, n):
-    """The small-batch boundary at K = 4096 on narrow N: the skinny kernel
-    below M = 8 (and below M = 24 for N <= 4096), the one-M-tile split-K
+    """The small-batch boundary at K = 4096 on narrow N: the narrow kernel
+    up to M = 16 (and up to M = 32 for N <= 4096), the one-M-tile split-K
     route above (with the module's workspace).  AUTO and the forced MFMA
     family equal the oracle bit for bit on both sides of each boundary."""
     ctx, mod, s = env
@@ -280,7 +280,7 @@ def test_decode_gemv_one_matrix_routes(env, k, n):
             check(bc, (bits(comb) >> 16).astype(np.uint16), "residual combined bf16")
 
 
-@pytest.mark.parametrize("m,n,k", [(129, 4096, 4096), (129, 24576, 4096), (16, 4096, 12288), (200, 6100, 4096),
+@pytest.mark.parametrize("m,n,k", [(129, 4096, 4096), (129, 24576, 4096), (24, 4096, 12288), (200, 6100, 4096),
                                    (64, 4096, 12288)])
 def test_diag_gemm_timeline_matches_linear(env, m, n, k):
     """The timed gemm_tall route (w8a8_diag_gemm_timeline) writes the BF16
@@ -637,23 +637,24 @@ def test_errors_raise_not_fall_back(env):
 
 # ------------------------------------------------------------------ split-K workspace
 @pytest.mark.parametrize("m,n,k", [(129, 4096, 12288), (512, 4096, 12288), (129, 4096, 4096), (129, 6144, 4096),
-                                   (16, 4096, 12288), (64, 4096, 12288), (40, 6144, 4096),
+                                   (24, 4096, 12288), (64, 4096, 12288), (40, 6144, 4096),
                                    (100, 96, 12288), (255, 1024, 4096), (100, 4096, 12288), (65, 4100, 12288),
                                    (128, 4096, 4096),
                                    (129, 4100, 4096), (64, 4100, 12288), (512, 4100, 12288),
-                                   (16, 4100, 12288), (100, 1024, 4096), (3, 4100, 12288), (7, 1024, 8192),
+                                   (17, 4100, 12288), (100, 1024, 4096), (3, 4100, 8448), (7, 1024, 8448),
                                    (255, 4096, 4096)])
 @pytest.mark.parametrize("dtype,res", [(np.float32, False), (np.uint16, True), (np.int32, False)])
 def test_linear_split_k_workspace_identical(env, m, n, k, dtype, res):
     """w8a8_linear_ex with a workspace (split-K partials + exact i32 epilogue)
     equals the call without one and the oracle, bit for bit -- also on a
     second call with the same workspace, which carries nothing between calls.
-    Below M = 16 only K >= 8192 splits (3 x 4100 x 12288 under AUTO's MFMA
-    route from M = 3, 7 x 1024 x 8192).
+    Up to M = 16 the narrow kernel takes every K it can split over its waves;
+    K >= 8192 with K % 1024 != 0 still splits there (3 x 4100 x 8448 under
+    AUTO's MFMA route from M = 3, 7 x 1024 x 8448).
     The shapes cover both slab policies with the 16-byte epilogue (M > 200,
     N % 8 == 0) and the 4-column one: streamed (gemm_tall from 3 MiB of
     slabs: 129 x 4096 x 4096 and 64 x 4100 x 12288 on 4 columns, 255 x 4096
-    x 4096 on 16 bytes) and plain (smaller gemm_tall sets such as 16 x 4100 x
+    x 4096 on 16 bytes) and plain (smaller gemm_tall sets such as 17 x 4100 x
     12288, 100 x 96 x 12288 and 100 x 1024 x 4096, and gemm_dma's split route
     above M = 256: 512 x 4096 x 12288 on 16 bytes, 512 x 4100 x 12288 on 4
     columns)."""
@@ -838,6 +839,55 @@ def test_linear_one_m_tile_wide_n(env, m, dtype, res):
         assert np.array_equal(outs[0][1], want)
     else:
         assert np.array_equal(bits(got), bits(of))
+
+
+
+@pytest.mark.parametrize("n,k", [(1000, 512), (4100, 4096), (333, 2048), (1000, 8192), (4096, 12288), (17, 12288)])
+@pytest.mark.parametrize("dtype,res", [(np.uint16, True), (np.float32, False), (np.int32, False)])
+def test_linear_narrow_every_m(env, n, k, dtype, res):
+    """The narrow kernel (small M on narrow N, K split over the workgroup's
+    waves, no slabs): M from 1 to 32 across its one to four live activation
+    loads per stage, four and eight waves (K below and from 8192), a
+    one-stage slice (K = 512), N not a multiple of 16; bit-exact against the
+    oracle in every output type, with the residual sum.  The forced MFMA
+    family runs it at M <= 2 (AUTO runs dot4 there); the route is checked
+    on the host."""
+    from inferrous_amd import _lib
+    ctx, mod, s = env
+    lib = _lib.lib()
+    dt = {np.float32: _lib.OUT_F32, np.uint16: _lib.OUT_BF16, np.int32: _lib.OUT_I32}[dtype]
+    took = 0
+    for m in (1, 2, 3, 8, 9, 16, 17, 24, 25, 32):
+        route = np.zeros(20, np.int32)
+        _lib.check(lib.w8a8_diag_linear_route(m, n, k, dt, int(res), _lib.PATH_MFMA, 0, route.ctypes.data, 20),
+                   "route")
+        took += int(route[0]) == 15
+        print(f"narrow m={m} n={n} k={k} {np.dtype(dtype).name} res={res} family={int(route[0])}", flush=True)
+        rng = np.random.default_rng(31 * m + n + k)
+        q = rng.integers(-127, 128, (m, k), dtype=np.int8)
+        w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        q[-1] = 127
+        w[-1] = -127
+        asc = (rng.random(m) / 64 + 1e-4).astype(F32)
+        ws = (rng.random(n) / 64 + 1e-4).astype(F32)
+        resid = oracle.bf16_rne(rng.standard_normal(m * n).astype(F32))
+        dq, da, dw, dws, dres = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws), dev(s, resid)
+        out = DeviceBuffer.zeroed(s, m * n, dtype)
+        comb = DeviceBuffer.zeroed(s, m * n, dtype) if res else None
+        _lib.check(lib.w8a8_linear_ex(s.handle, dq.ptr, da.ptr, m, dw.ptr, dws.ptr, n, k,
+                                      dres.ptr if res else None, out.ptr, comb.ptr if res else None, dt,
+                                      _lib.PATH_MFMA, None, 0))
+        acc, of, ob = oracle.linear(q, asc, w, ws, k, threads=8)
+        got = out.to_host_vec(s)
+        if dtype == np.int32:
+            assert np.array_equal(got, acc), f"m={m}"
+        elif dtype == np.uint16:
+            assert np.array_equal(got, ob), f"m={m}"
+            want = (bits(oracle.residual(resid, of)) >> 16).astype(np.uint16)
+            assert np.array_equal(comb.to_host_vec(s), want), f"m={m} combined"
+        else:
+            assert np.array_equal(bits(got), bits(of)), f"m={m}"
+    assert took >= 6
 
 
 @pytest.mark.parametrize("n,tile", [(23100, "256x192"), (15300, "128x192"), (6200, "128x128"), (1000, "128x64")])

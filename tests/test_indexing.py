@@ -280,6 +280,63 @@ def check_skinny(m, n, k, r):
     written_once("gemm_skinny out", rr[keep] * n + cc[keep], m * n)
 
 
+def check_narrow(m, n, k, r):
+    """gemm_narrow (gemm.hip:284-372, plan :1135): grid ceil(n / 16) x 64 S
+    threads; wave w sums K slice [w K / S, (w + 1) K / S) in 128-byte stages
+    through its own R-stage ring; DMA instruction j < 2 + LAL fills rows
+    8j .. 8j + 7 of a stage (lane l: row 8j + l / 8, global chunk
+    (l % 8) ^ (row % 8)); rows 0-15 are weight rows n0 + row clamped to
+    n - 1, rows 16.. activation rows row - 16, loaded only below M."""
+    MB, S, LAL, R = r["mt"], r["s"], r["u"], r["sa"]
+    assert r["grid_x"] == -(-n // 16) and r["grid_y"] == 1 and r["block"] == 64 * S and r["splits"] == 1
+    assert k % (128 * S) == 0 and 16 * MB >= m
+    # every row below M has its DMA instruction, and every issued instruction has a live lane
+    assert 8 * LAL >= m and 8 * (LAL - 1) < m, (m, LAL)
+    ROWS, L = 16 * (1 + MB), 2 + LAL
+    STAGE, RING = ROWS * 128, R * ROWS * 128
+    assert L <= ROWS // 8 and S * RING <= 160 * 1024
+    KS = k // S
+    ST = KS // 128
+    n0 = np.arange(r["grid_x"])[:, None] * 16
+    lane = np.arange(64)
+    for wave in range(S):
+        for st in ({0, ST - 1} if ST > 0 else set()):
+            for j in range(L):
+                row = 8 * j + (lane >> 3)
+                chunk = ((lane & 7) ^ (row & 7)) * 16
+                koff = wave * KS + st * 128 + chunk
+                if j < 2:
+                    src = np.minimum(n0 + row, n - 1) * k + koff
+                    within("gemm_narrow W", src, src + 16, n * k)
+                else:
+                    g = row - 16
+                    live = g < m
+                    src = (g * k + koff)[live]
+                    within("gemm_narrow A", src, src + 16, m * k)
+                dst = wave * RING + (st % R) * STAGE + j * 1024 + lane * 16
+                within("gemm_narrow LDS DMA", dst, dst + 16, S * RING)
+    fr, fq = lane & 15, lane >> 4
+    for h in range(2):
+        c = 4 * h + fq
+        b = fr * 128 + ((c ^ (fr & 7)) * 16)
+        within("gemm_narrow B fragments", b, b + 16, STAGE)
+        for t in range(MB):
+            row = 16 + 16 * t + fr
+            a = row * 128 + ((c ^ (row & 7)) * 16)
+            within("gemm_narrow A fragments", a, a + 16, STAGE)
+    red = ((np.arange(S)[:, None, None, None] * MB + np.arange(MB)[:, None, None]) * 4
+           + np.arange(4)[:, None]) * 64 + lane
+    within("gemm_narrow reduction", red * 4, red * 4 + 4, S * RING)
+    # epilogue: index i = tid, tid + 64 S, ... < MB * 256 -> (t, v, l)
+    i = np.arange(MB * 4 * 64)
+    l, v, t = i & 63, (i >> 6) & 3, i >> 8
+    rr = 16 * t + 4 * (l >> 4) + v
+    cc = n0 + (l & 15)
+    rr = np.broadcast_to(rr, cc.shape)
+    keep = (rr < m) & (cc < n)
+    written_once("gemm_narrow out", rr[keep] * n + cc[keep], m * n)
+
+
 def check_tiled(m, n, k, r):
     """gemm_tiled (gemm.hip:138-232): guarded 16-byte loads (gm < M, kk < K),
     LDS rows of PITCH = 144 bytes, XCD-aware tile numbering."""
@@ -402,6 +459,8 @@ def check_linear(m, n, k, dtype=BF16, residual=False, path=AUTO, workspace=0):
         check_dma(m, n, k, r, residual)
     elif fam == 14:
         check_tiled(m, n, k, r)
+    elif fam == 15:
+        check_narrow(m, n, k, r)
     else:
         raise AssertionError(f"no route for {(m, n, k)}: {r}")
     return r
@@ -472,14 +531,31 @@ def test_k_not_multiple_of_128(m, n, k):
     check_linear(m, n, k, path=DOT4)
 
 
+@pytest.mark.parametrize("n,k", [(4096, 4096), (6144, 4096), (4096, 12288), (1000, 512), (4100, 8192), (333, 2048),
+                                 (17, 12288)])
+def test_narrow_every_m(n, k):
+    """gemm_narrow at every M it takes (1-16, and 17-32 at K <= 4096 on
+    N <= 4096): both wave counts (K below and from 8192), one to four live
+    activation loads per stage, N not a multiple of 16, a one-stage slice
+    (K = 512)."""
+    took = 0
+    for m in range(1, 33):
+        for path in (AUTO, MFMA):
+            r = check_linear(m, n, k, path=path, workspace=workspace_bytes(m, n, k))
+            if path == MFMA and m <= 16:
+                assert r["family"] == 15, (m, n, k, r)
+            took += r["family"] == 15
+    assert took >= 16
+
+
 def test_every_family_is_replayed():
     """The shapes above reach every GEMM and GEMV family."""
     seen = set()
-    for (m, n, k, ws) in [(1, 4096, 4096, 0), (1, 4096, 1040, 0), (3, 4096, 4096, 0), (129, 4096, 4096, 1 << 30),
-                          (512, 24576, 4096, 0), (100, 4096, 4112, 0)]:
+    for (m, n, k, ws) in [(1, 4096, 4096, 0), (1, 4096, 1040, 0), (3, 4096, 4096, 0), (3, 4096, 1040, 0),
+                          (129, 4096, 4096, 1 << 30), (512, 24576, 4096, 0), (100, 4096, 4112, 0)]:
         seen.add(route(m, n, k, workspace=ws)["family"])
     seen.add(argmax_route(4096, 4096)["family"])
-    assert seen == {1, 2, 3, 11, 12, 13, 14}, seen
+    assert seen == {1, 2, 3, 11, 12, 13, 14, 15}, seen
 
 
 # ------------------------------------------------------------------ folded producers
@@ -569,3 +645,15 @@ def test_checker_catches_planted_mistakes():
         written_once("block rows", (wrong * 32 + (lane2 & 31)).ravel(), 32 * 32)
     rows, cols = mfma32_rows_cols(lane2, v)
     written_once("block rows", (rows * 32 + np.broadcast_to(cols, rows.shape)).ravel(), 32 * 32)
+    # gemm_narrow: activation rows loaded without the live mask (M = 3: rows 3-7 of the first
+    # activation instruction), and a live-load count one short of the rows (M = 9, LAL = 1)
+    m, n, k = 3, 4096, 4096
+    r = route(m, n, k, path=MFMA)
+    assert r["family"] == 15
+    g = (8 * 2 + (lane >> 3)) - 16
+    src = g * k + ((lane & 7) ^ ((g + 16) & 7)) * 16 + (r["s"] - 1) * (k // r["s"])
+    with pytest.raises(AssertionError, match="past the buffer"):
+        within("unmasked A", src, src + (k // r["s"] - 128) + 16, m * k)
+    bad = dict(route(9, n, k, path=MFMA), u=1)
+    with pytest.raises(AssertionError):
+        check_narrow(9, n, k, bad)
