@@ -1130,8 +1130,10 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
 // qkv 6144 x 4096 at M = 2 / 8 / 16 6.98 / 7.48 / 8.09 against 8.30 / 8.98 /
 // 9.25 (S = 4; 8.50 / 9.17 / 9.59 with S = 8).  At M = 24 and 32 down and
 // qkv are level or slower than gemm_tall (down 13.78 / 15.12 against 13.59 /
-// 14.03) and keep it.  Deeper rings (5) and 16 waves measured level or
-// slower.
+// 14.03) and keep it.  gate_up (24576 x 4096, 1,536 workgroups) measured
+// slower on it (M = 4 / 8 / 16 19.31 / 19.86 / 21.74 us against 18.23 /
+// 18.01 / 17.41 on the 96-column tiles).  Deeper rings (5) and 16 waves
+// measured level or slower.
 static bool narrow_plan(uint32_t m, uint32_t n, uint32_t k, int& S, int& R, int& MB, int& LAL) {
   if (m == 0 || m > 32 || (n + 95) / 96 >= 224) return false;
   S = k >= 8192 ? 8 : 4;
