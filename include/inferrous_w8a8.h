@@ -204,8 +204,9 @@ int w8a8_linear_path(void *stream, const int8_t *q, const float *asc, size_t m,
  * not overlap. */
 size_t w8a8_linear_workspace_bytes(size_t m, size_t n, uint32_t k);
 /* The same for one route: 0 for W8A8_PATH_DOT4, and for W8A8_PATH_AUTO
- * where AUTO runs the dot4 GEMV whatever the workspace (m <= 2); the MFMA
- * family's need otherwise.  Size a per-call workspace with this. */
+ * where AUTO runs the dot4 GEMV whatever the workspace (m = 1, and m = 2
+ * unless the MFMA route there is the narrow kernel or the unsplit one-M-tile
+ * kernel, which need none); the MFMA family's need otherwise.  Size a per-call workspace with this. */
 size_t w8a8_linear_workspace_bytes_path(size_t m, size_t n, uint32_t k, int path);
 /* The largest w8a8_linear_workspace_bytes(m, n, k) over m = 1 .. max_m.
  * The need is not monotone in m: 6144 x 4096 needs 25.2 MB at m = 256 and

@@ -65,25 +65,37 @@ int check_linear(const int8_t* q, const float* asc, size_t m, const int8_t* w, c
   return W8A8_OK;
 }
 
-// AUTO route of one projection: the dot4 GEMV for m <= 2, the MFMA family
-// from m = 3.  Measured on MI355X through this ABI (graphs of 16
-// distinct-weight launches, random operands), dot4 against MFMA at
-// m = 2 / 3 / 4: qkv 7.7 / 8.9 / 9.3 against 8.4 / 8.6 / 8.8 us, o 5.85 /
-// 7.3 / 7.45 against 7.1 / 7.1 / 7.2, gate_up 17.7 / 19.7 / 20.6 against
-// 18.0 / 18.0 / 18.0, down 11.7 / 14.0 / 14.4 against 13.2 / 13.3 / 13.4.
-// Down's MFMA figure is its split-K plan, which needs the caller's
-// workspace; without it (16.8 us) m = 3 and 4 keep the dot4 GEMV.  The
-// grouped projections keep one dot4 launch for every matrix up to m = 4
-// (kDot4MaxM).
+// AUTO route of one projection: the dot4 GEMV at m = 1; at m = 2 the MFMA
+// family where it runs gemm_narrow or gemm_tall, the dot4 GEMV otherwise;
+// the MFMA family from m = 3.  Measured on MI355X through this ABI (graphs of
+// 36 distinct-weight launches, random operands), dot4 against MFMA at
+// m = 1 / 2 / 3 / 4: qkv 5.46 / 7.35 / 8.58 / 9.00 against 6.92 / 7.00 /
+// 7.05 / 7.17 us, o 4.36 / 5.71 / 7.13 / 7.26 against 5.50 / 5.49 / 5.51 /
+// 5.54, gate_up 15.85 / 17.58 / 19.69 / 20.59 against 17.15 / 17.16 / 17.19
+// / 17.21, down 8.81 / 11.55 / 13.90 / 14.28 against 10.96 / 11.01 / 11.05 /
+// 11.09 (gemm_narrow on qkv, o and down, gemm_tall on gate_up).  The other
+// MFMA routes at m = 2 (gemm_skinny at K not a multiple of 512, split-K) were
+// not measured to lead and keep the GEMV.  A split-K route needs the
+// caller's workspace; without it m = 3 and 4 keep the dot4 GEMV.  The grouped
+// projections keep one dot4 launch for every matrix up to m = 4 (kDot4MaxM).
 constexpr size_t kDot4MaxM = 4;
 constexpr size_t kDot4AutoMaxM = 2;
 constexpr size_t kRowtailWidthAbi = 12288;  // the down projection's K (the MLP width)
 
 static int auto_path(size_t m, size_t n, uint32_t k, size_t workspace_bytes) {
-  if (m <= kDot4AutoMaxM) return W8A8_PATH_DOT4;
+  if (m < kDot4AutoMaxM) return W8A8_PATH_DOT4;
   if (m > kDot4MaxM) return W8A8_PATH_MFMA;
   const size_t need = gemm_workspace_bytes((uint32_t)m, (uint32_t)n, k);
-  return need == 0 || workspace_bytes >= need ? W8A8_PATH_MFMA : W8A8_PATH_DOT4;
+  if (need != 0 && workspace_bytes < need) return W8A8_PATH_DOT4;
+  if (m == kDot4AutoMaxM) {
+    GemmArgs g{};
+    g.m = (uint32_t)m;
+    g.n = (uint32_t)n;
+    g.k = k;
+    const int family = gemm_route(g).family;
+    return family == kRouteNarrow || (family == kRouteTall && need == 0) ? W8A8_PATH_MFMA : W8A8_PATH_DOT4;
+  }
+  return W8A8_PATH_MFMA;
 }
 
 int run_linear(hipStream_t st, const int8_t* q, const float* asc, size_t m, const int8_t* w,
@@ -522,7 +534,8 @@ size_t w8a8_linear_workspace_bytes(size_t m, size_t n, uint32_t k) {
 
 size_t w8a8_linear_workspace_bytes_path(size_t m, size_t n, uint32_t k, int path) {
   if (path == W8A8_PATH_DOT4) return 0;
-  if (path == W8A8_PATH_AUTO && m <= kDot4AutoMaxM) return 0;  // AUTO runs the dot4 GEMV there
+  if (path == W8A8_PATH_AUTO && m <= kDot4AutoMaxM && auto_path(m, n, k, 0) == W8A8_PATH_DOT4)
+    return 0;  // AUTO runs the dot4 GEMV there
   if (path != W8A8_PATH_AUTO && path != W8A8_PATH_MFMA) return 0;
   return w8a8_linear_workspace_bytes(m, n, k);
 }

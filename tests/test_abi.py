@@ -524,7 +524,7 @@ def test_noalloc_argmax_validation():
 def test_workspace_queries_by_route_and_batch_range():
     """The split-K workspace need depends on the route and is not monotone
     in M: the narrow kernel (M <= 16 on down) needs none, the one-M-tile
-    split-K route above it does, AUTO at M <= 2 runs the dot4 GEMV, DOT4
+    split-K route above it does, AUTO at M = 1 runs the dot4 GEMV, DOT4
     never needs any, MFMA keeps the shape's need; the largest need over
     M = 1..512 for qkv (6144 x 4096) sits at M = 256, where M = 512 needs
     none."""

@@ -801,8 +801,8 @@ def test_linear_one_m_tile_wide_n(env, m, dtype, res):
     32 x 32 block per wave up to M = 64 (one to six blocks busy) and 32-row
     slices above, waves without work idle, activation rows past M never
     loaded, a ragged last column tile; bit-exact against the oracle with and
-    without a workspace.  M <= 2 forces the MFMA family (AUTO runs dot4
-    there)."""
+    without a workspace.  M <= 2 forces the MFMA family (AUTO runs dot4 at
+    M = 1)."""
     from inferrous_amd import _lib
     ctx, mod, s = env
     n, k = 21601, 1024
@@ -850,7 +850,7 @@ def test_linear_narrow_every_m(env, n, k, dtype, res):
     loads per stage, four and eight waves (K below and from 8192), a
     one-stage slice (K = 512), N not a multiple of 16; bit-exact against the
     oracle in every output type, with the residual sum.  The forced MFMA
-    family runs it at M <= 2 (AUTO runs dot4 there); the route is checked
+    family runs it at M = 1 (AUTO runs dot4 there); the route is checked
     on the host."""
     from inferrous_amd import _lib
     ctx, mod, s = env
