@@ -1094,27 +1094,6 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
   return kt % splits == 0 && kt / splits >= 4;
 }
 
-// gemm_tall plan for 1 <= m <= 256 (measured on MI355X on the Qwen3-8B
-// projection shapes at M = 16, 64, 65, 80, 100, 128 and 129): 96-column
-// tiles when they alone give about one tile per CU; otherwise split K four
-// ways (two when K is short), with 96- or 64-column tiles, to reach about one
-// workgroup per CU.  For 64 < m <= 128 one 160-row tile streams the weights
-// once where gemm_dma's two 64-row tiles stream them twice (gate_up at
-// M = 100 24.6-24.9 against 33.3-34.1 us, down 20.7 against 23.3-23.5), and
-// with streamed slabs the split route also beats gemm_dma's split-K 2 on
-// qkv and o (qkv at M = 65 / 100 / 128 12.6 / 14.1 / 14.5 against
-// 13.2-13.3 / 14.6 / 15.5, o 10.9 / 11.6 / 12.7 against 12.0 / 12.7 / 13.2).
-// At small m the plan applies to the wide shapes and to long K at any m,
-// where it beats gemm_skinny (graphs of 16 distinct-weight launches, random
-// operands, m = 1..6: gate_up 17.9-18.1 against 21.2-24.0 us, down at
-// K = 12288 13.1-13.5 against 16.7-17.1).  At K = 4096 on narrow N the
-// skinny kernel (one workgroup per 16 columns) leads while its grid fits the
-// CUs once: o (4096 columns) at m = 2 / 4 / 8 / 12 / 16 / 24 7.1 / 7.2 /
-// 7.4 / 7.6 / 7.9 / 9.6 us against 7.8 / 7.8 / 8.0 / 8.0 / 8.2 / 9.0; qkv
-// (6144 columns) 8.4 / 8.8 / 9.6 / 10.5 / 11.5 against 8.6 / 8.8 / 9.0 /
-// 9.1 / 9.3, so it takes this plan from m = 8, o from m = 24.
-// Returns false when no plan applies (the gemm_dma or gemm_skinny routes
-// then run).  ma: the M tile (64, 160 or 256 rows).
 // gemm_narrow's plan: S = 4 waves below K = 8192 and 8 from there (each wave
 // keeps eight or more 128-byte stages), R-deep rings, MB 16-row blocks, LAL
 // = ceil(M / 8) activation DMA loads per stage.  It takes M <= 16 on the
@@ -1145,6 +1124,29 @@ static bool narrow_plan(uint32_t m, uint32_t n, uint32_t k, int& S, int& R, int&
   return true;
 }
 
+
+// gemm_tall plan for 1 <= m <= 256 (measured on MI355X on the Qwen3-8B
+// projection shapes at M = 16, 64, 65, 80, 100, 128 and 129): 96-column
+// tiles when they alone give about one tile per CU; otherwise split K four
+// ways (two when K is short), with 96- or 64-column tiles, to reach about one
+// workgroup per CU.  For 64 < m <= 128 one 160-row tile streams the weights
+// once where gemm_dma's two 64-row tiles stream them twice (gate_up at
+// M = 100 24.6-24.9 against 33.3-34.1 us, down 20.7 against 23.3-23.5), and
+// with streamed slabs the split route also beats gemm_dma's split-K 2 on
+// qkv and o (qkv at M = 65 / 100 / 128 12.6 / 14.1 / 14.5 against
+// 13.2-13.3 / 14.6 / 15.5, o 10.9 / 11.6 / 12.7 against 12.0 / 12.7 / 13.2).
+// At small m the plan applies to the wide shapes and to long K at any m,
+// where it beats gemm_skinny (graphs of 16 distinct-weight launches, random
+// operands, m = 1..6: gate_up 17.9-18.1 against 21.2-24.0 us, down at
+// K = 12288 13.1-13.5 against 16.7-17.1).  At K = 4096 on narrow N the
+// skinny kernel (one workgroup per 16 columns) led while its grid fits the
+// CUs once: o (4096 columns) at m = 2 / 4 / 8 / 12 / 16 / 24 7.1 / 7.2 /
+// 7.4 / 7.6 / 7.9 / 9.6 us against 7.8 / 7.8 / 8.0 / 8.0 / 8.2 / 9.0; qkv
+// (6144 columns) 8.4 / 8.8 / 9.6 / 10.5 / 11.5 against 8.6 / 8.8 / 9.0 /
+// 9.1 / 9.3, so it takes this plan from m = 8, o from m = 24.  gemm_narrow's
+// plan, checked first, now takes the small batches on narrow N.
+// Returns false when no plan applies (the gemm_dma or gemm_skinny routes
+// then run).  ma: the M tile (64, 160 or 256 rows).
 static bool tall_plan(uint32_t m, uint32_t n, uint32_t k, int& bn, uint32_t& splits, int& ma) {
   if (m == 0 || m > 256 || k % 128 != 0) return false;
   ma = m <= 64 ? 64 : m <= 160 ? 160 : 256;

@@ -82,13 +82,13 @@ def xcd_slot(b, G):
 
 
 def mfma32_rows_cols(lane, v):
-    """Row / column of value v of lane l in a 32 x 32 i32 MFMA block (gemm.hip:259-261)."""
+    """Row / column of value v of lane l in a 32 x 32 i32 MFMA block (gemm.hip:374-376)."""
     return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3), lane & 31
 
 
 def frag_offsets():
     """gemm_dma / gemm_tall fragment reads: lane l, sub-step i -> byte offset
-    inside a 32-row block of 128-byte LDS rows (gemm.hip:441-443, :686-688)."""
+    inside a 32-row block of 128-byte LDS rows (gemm.hip:551-554, :821-824)."""
     lane = np.arange(64)
     fr, fh = lane & 31, lane >> 5
     return np.stack([fr * 128 + (((2 * i + fh) ^ ((fr >> 1) & 7)) * 16) for i in range(4)])  # [4, 64]
@@ -98,7 +98,7 @@ def frag_offsets():
 def store_blocks(m, n, row0, col0, FM, FN):
     """(rows, cols) that store_blocks writes for wave tiles with top-left
     corners (row0, col0) (broadcast arrays), guarded by r < m, c < n
-    (gemm.hip:266-337).  Its epilogue loads are clamped (min(r, m - 1),
+    (gemm.hip:381-452).  Its epilogue loads are clamped (min(r, m - 1),
     min(c, n - 1)), hence always in bounds."""
     lane = np.arange(64)[:, None]
     v = np.arange(16)[None, :]
@@ -113,7 +113,7 @@ def store_blocks(m, n, row0, col0, FM, FN):
 
 
 def check_dma(m, n, k, r, residual):
-    """gemm_dma (gemm.hip:360-506) over its grid: DMA sources, LDS ring slots,
+    """gemm_dma (gemm.hip:475-621) over its grid: DMA sources, LDS ring slots,
     fragment reads, the stores of store_blocks."""
     BM, BN, WM, WN, SA, SB, splits = r["bm"], r["bn"], r["wm"], r["wn"], r["sa"], r["sb"], r["splits"]
     tm, tn = -(-m // BM), -(-n // BN)
@@ -164,7 +164,7 @@ def check_dma(m, n, k, r, residual):
 
 
 def check_tall(m, n, k, r, residual):
-    """gemm_tall (gemm.hip:619-798): per-wave DMA instruction dealing, the
+    """gemm_tall (gemm.hip:738-937): per-wave DMA instruction dealing, the
     rings, the two compute mappings, the stores."""
     BN, SA, SB, MA, splits = r["bn"], r["sa"], r["sb"], r["ma"], r["splits"]
     FN, ASL, BSL, NB = BN // 32, MA * 128, BN * 128, BN // 8
@@ -229,7 +229,7 @@ def check_tall(m, n, k, r, residual):
 
 
 def check_epilogue(m, n, r, residual):
-    """splitk_epilogue / splitk_epilogue8 (gemm.hip:813-930): grid
+    """splitk_epilogue / splitk_epilogue8 (gemm.hip:952-1085): grid
     (ceil(n / cols / 256), min(m, 65535)), thread columns c .. c + cols - 1,
     rows blockIdx.y, + gridDim.y, ...; slab index clamped to splits - 1."""
     cols, splits = r["epi_cols"], r["splits"]
@@ -249,7 +249,7 @@ def check_epilogue(m, n, r, residual):
 
 
 def check_skinny(m, n, k, r):
-    """gemm_skinny (gemm.hip:83-135): grid (ceil(n / 16), 1), S waves split K in
+    """gemm_skinny (gemm.hip:92-144): grid (ceil(n / 16), 1), S waves split K in
     64-byte steps; loads guarded by kk + koff < K (16-byte reads, K % 16 == 0)."""
     MT, S, U = r["mt"], r["s"], r["u"]
     assert r["grid_x"] == -(-n // 16) and r["grid_y"] == 1 and 16 * MT >= m and k % 16 == 0
@@ -281,7 +281,7 @@ def check_skinny(m, n, k, r):
 
 
 def check_narrow(m, n, k, r):
-    """gemm_narrow (gemm.hip:284-372, plan :1135): grid ceil(n / 16) x 64 S
+    """gemm_narrow (gemm.hip:268-372, plan :1116): grid ceil(n / 16) x 64 S
     threads; wave w sums K slice [w K / S, (w + 1) K / S) in 128-byte stages
     through its own R-stage ring; DMA instruction j < 2 + LAL fills rows
     8j .. 8j + 7 of a stage (lane l: row 8j + l / 8, global chunk
@@ -338,7 +338,7 @@ def check_narrow(m, n, k, r):
 
 
 def check_tiled(m, n, k, r):
-    """gemm_tiled (gemm.hip:138-232): guarded 16-byte loads (gm < M, kk < K),
+    """gemm_tiled (gemm.hip:147-241): guarded 16-byte loads (gm < M, kk < K),
     LDS rows of PITCH = 144 bytes, XCD-aware tile numbering."""
     BM, BN, WM, WN = r["bm"], r["bn"], r["wm"], r["wn"]
     PITCH = 144
@@ -389,7 +389,7 @@ def check_tiled(m, n, k, r):
 
 # ------------------------------------------------------------------ GEMV routes
 def check_gemv_m1(m, n, k, r, residual, argmax=False):
-    """gemv_m1_one / gemv_m1 (gemv.hip:196-318): wave g owns rows R g ..
+    """gemv_m1_one / gemv_m1 (gemv.hip:205-325): wave g owns rows R g ..
     R g + R - 1; loads clamped to n - 1; lanes < R store rows < n."""
     R, KC, W = r["rows"], r["kc"], r["waves"]
     assert m == 1 and k == KC * 1024
@@ -414,7 +414,7 @@ def check_gemv_m1(m, n, k, r, residual, argmax=False):
 
 
 def check_gemv_mt(m, n, k, r, residual):
-    """gemv_mt (gemv.hip:347-431): 4-row groups, MT activation rows per pass
+    """gemv_mt (gemv.hip:348-423): 4-row groups, MT activation rows per pass
     (blockIdx.y), 1 KiB chunks with rotation, loads guarded by kk < K."""
     MT, R = r["mt"], 4
     groups = -(-n // R)
@@ -560,8 +560,8 @@ def test_every_family_is_replayed():
 
 # ------------------------------------------------------------------ folded producers
 def check_rows_split(n, NS, RS, K):
-    """gemv_m1_split / gemv_rowtail_split streaming waves (gemv.hip:683-760,
-    :845-960): row r of wave wv of workgroup b is (r NS + wv) G + slot(b),
+    """gemv_m1_split / gemv_rowtail_split streaming waves (gemv.hip:690-757,
+    :856-965): row r of wave wv of workgroup b is (r NS + wv) G + slot(b),
     loads clamped to n - 1, stores guarded by row < n."""
     G = -(-n // (NS * RS))
     b, wv, rr = np.meshgrid(np.arange(G), np.arange(NS), np.arange(RS), indexing="ij")
@@ -574,7 +574,7 @@ def check_rows_split(n, NS, RS, K):
 
 
 def check_swiglu_split(n, NS=12, CS=4):
-    """gemv_swiglu_split (gemv.hip:762-843): coordinate k of wave wv of
+    """gemv_swiglu_split (gemv.hip:763-842): coordinate k of wave wv of
     workgroup b is (k NS + wv) G + slot(b)."""
     G = -(-n // (NS * CS))
     b, wv, kk = np.meshgrid(np.arange(G), np.arange(NS), np.arange(CS), indexing="ij")
