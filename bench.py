@@ -182,11 +182,14 @@ def prefill_profile_run() -> int:
 
 
 def ragged_profile_run() -> int:
-    """Workload for a kernel-trace profile of the ragged small batches
-    (config 5): 8 layers of distinct gate_up and down weights (1.2 GB), M = 4,
-    16 and 64 per-row-seeded rows, the dot4 GEMV and the MFMA GEMM forced in
-    turn, three eager passes each (no graphs)."""
+    """Workload for a kernel-trace or counter profile of the ragged small
+    batches (config 5): 8 layers of distinct gate_up and down weights (1.2 GB),
+    M = 4, 16 and 64 per-row-seeded rows, the dot4 GEMV and the MFMA GEMM
+    forced in turn, three eager passes each (no graphs); then a 256 MiB device
+    copy three times, the calibration kernel of known traffic for counter
+    passes (reads and writes 256 MiB)."""
     from inferrous_amd import CudaContext, DeviceBuffer, load, synth
+    from inferrous_amd import _lib
     ctx = CudaContext(0)
     mod = load(ctx)
     s = ctx.new_stream()
@@ -215,6 +218,12 @@ def ragged_profile_run() -> int:
                     getattr(mod, fam)(s, None, pq[k][0], pq[k][1], w, ws, k, outs[name])
             s.synchronize()
             print(f"ragged M={m} {fam} done", flush=True)
+    src = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
+    dst = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
+    for _ in range(3):
+        _lib.check(_lib.lib().w8a8_memcpy_dtod(dst.ptr, src.ptr, 256 << 20, s.handle), "memcpy_dtod")
+    s.synchronize()
+    print("calibration copies done", flush=True)
     return 0
 
 
