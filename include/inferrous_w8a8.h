@@ -52,9 +52,10 @@ extern "C" {
 #define W8A8_OUT_I32 2  /* raw exact INT32 accumulators, no epilogue          */
 
 /* kernel family selection for w8a8_linear_path (tests/bench); AUTO is what
- * w8a8_linear uses: the dot4 GEMV up to M = 2, the MFMA family from M = 3
- * (at M = 3 and 4 the dot4 GEMV when the shape's split-K plan needs a
- * workspace the call did not give) */
+ * w8a8_linear uses: the dot4 GEMV at M = 1; at M = 2 the MFMA family where
+ * its route is the narrow kernel or the unsplit one-M-tile kernel, the dot4
+ * GEMV otherwise; the MFMA family from M = 3 (at M = 3 and 4 the dot4 GEMV
+ * when the shape's split-K plan needs a workspace the call did not give) */
 #define W8A8_PATH_AUTO 0
 #define W8A8_PATH_DOT4 1 /* v_dot4 GEMV, wave per row group           */
 #define W8A8_PATH_MFMA 2 /* MFMA GEMM: LDS-staged v_mfma_i32_32x32x32_i8,

@@ -66,8 +66,8 @@ int check_linear(const int8_t* q, const float* asc, size_t m, const int8_t* w, c
 }
 
 // AUTO route of one projection: the dot4 GEMV at m = 1; at m = 2 the MFMA
-// family where it runs gemm_narrow or gemm_tall, the dot4 GEMV otherwise;
-// the MFMA family from m = 3.  Measured on MI355X through this ABI (graphs of
+// family where it runs gemm_narrow or an unsplit gemm_tall, the dot4 GEMV
+// otherwise; the MFMA family from m = 3.  Measured on MI355X through this ABI (graphs of
 // 36 distinct-weight launches, random operands), dot4 against MFMA at
 // m = 1 / 2 / 3 / 4: qkv 5.46 / 7.35 / 8.58 / 9.00 against 6.92 / 7.00 /
 // 7.05 / 7.17 us, o 4.36 / 5.71 / 7.13 / 7.26 against 5.50 / 5.49 / 5.51 /
