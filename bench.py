@@ -586,10 +586,19 @@ def main() -> int:
         return g
 
     def time_graph(g: Graph, reps: int, warm: int = 2) -> float:
-        """Median-free mean over reps of graph replays, HIP events on `s` (ms)."""
-        for _ in range(warm):
-            g.launch()
-        s.synchronize()
+        """Mean over reps of graph replays, HIP events on `s` (ms), after at
+        least `warm` replays and WARM_SECONDS of them.  Measured on MI355X: the
+        36-layer prefill graphs timed after one warm replay, with the device
+        idle for 0.5 s before (as after the host builds the next inputs), took
+        5.02 ms at M = 512 and 2.92 ms at M = 129; after 0.3 s of replays
+        4.81-4.83 and 2.65 ms, and the same after a further second."""
+        t0 = time.perf_counter()
+        done = 0
+        while done < warm or time.perf_counter() - t0 < WARM_SECONDS:
+            for _ in range(4):
+                g.launch()
+            done += 4
+            s.synchronize()
         e0, e1 = Event(), Event()
         e0.record(s)
         for _ in range(reps):
@@ -704,9 +713,12 @@ def main() -> int:
         seq_entries.append(dict(q=qs[hk][0], asc=qs[hk][1], w=head_w, ws=head_s, out=None, select=True))
         plan = mod.prepare_sequence(seq_entries)
         seq_token = DeviceBuffer.zeroed(s, 1, np.uint32)
-        for _ in range(20):
-            mod.linear_sequence(s, plan, seq_token)
-        s.synchronize()
+        seq_t0, seq_warm = time.perf_counter(), 0
+        while seq_warm < 20 or time.perf_counter() - seq_t0 < WARM_SECONDS:
+            for _ in range(10):
+                mod.linear_sequence(s, plan, seq_token)
+            seq_warm += 10
+            s.synchronize()
         e0, e1 = Event(), Event()
         e0.record(s)
         for _ in range(50):
