@@ -39,9 +39,9 @@
 //    split-K on narrow n.
 //  * gemm_narrow (M <= 16, or M <= 32 on n <= 4096 at k <= 4096, where the
 //    n / 96 tiles are fewer than 224 and k splits into S slices of 128-byte
-//    stages): one workgroup owns 16 weight rows; its S waves split K into S
-//    slices, and each wave streams its slice through its own global -> LDS
-//    ring (16 weight rows and the live activation rows of a 128-byte stage,
+//    stages): one workgroup owns 16 weight rows; its S waves split K
+//    (contiguous slices at S = 4, interleaved 128-byte chunks at S = 8), and
+//    each wave streams its share through its own global -> LDS ring (16 weight rows and the live activation rows of a 128-byte stage,
 //    global_load_lds_dwordx4: eight whole lines per instruction), so the K
 //    loop has no workgroup barrier and no split-K slabs leave the CU.  The S
 //    partial 16 x 16 tiles are summed through LDS (exact) and stored by the
@@ -267,9 +267,17 @@ constexpr bool raw_i32(int ep) { return ep == EP_I32 || ep == EP_SLAB; }
 
 // ---------------------------------------------------------------- narrow
 // Workgroup b owns output columns [16 b, 16 b + 16) and all M rows (MB
-// 16-row blocks).  Wave w sums the K slice [w K / S, (w + 1) K / S) in
-// 128-byte stages (the host guarantees K % (128 S) == 0) through its own
-// ring of R stages: a stage holds 16 weight rows, then 16 MB activation
+// 16-row blocks).  Wave w sums ST = K / (128 S) of the 128-byte K chunks
+// (the host guarantees K % (128 S) == 0): with S = 4 the contiguous slice
+// w ST .. w ST + ST - 1, stage s reading chunk w ST + s; with S = 8 the
+// waves interleave, stage s reading chunk ((s + b) mod ST) S + w, so that a
+// workgroup's eight waves read eight consecutive chunks of every row and
+// workgroups start at different chunks (down 4096 x 12288 at M = 2 / 8 / 16,
+// graphs of 36 launches on MI355X: 10.90 / 10.93 / 11.98 us against 11.03 /
+// 11.27 / 12.32 for contiguous slices; at K = 4096 with S = 4 the
+// interleaved order was 0.4-0.8 us slower on qkv and o).  Each wave streams
+// its chunks through its own ring of R stages: a stage holds 16 weight rows,
+// then 16 MB activation
 // rows, 128 bytes each; DMA instruction j fills rows 8j .. 8j + 7, lane l
 // chunk l % 8 of row 8j + l / 8 with global chunk (l % 8) ^ (row % 8), so
 // that the 16-row fragment reads (lane l: row l % 16) meet eight distinct
@@ -295,8 +303,7 @@ __global__ __launch_bounds__(64 * S) void gemm_narrow(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const uint32_t n0 = blockIdx.x * 16, K = a.k, M = a.m, N = a.n;
-  const uint32_t KS = K / S, ST = KS / 128;
-  const size_t k0 = (size_t)wave * KS;
+  const uint32_t ST = K / (128 * S);
   int8_t* const ring = lds + wave * RING;
 
   const int8_t* src[L];
@@ -307,20 +314,21 @@ __global__ __launch_bounds__(64 * S) void gemm_narrow(GemmArgs a) {
     const size_t chunk = (size_t)(((lane & 7) ^ (row & 7)) * 16);
     if (row < 16) {
       const uint32_t g = n0 + row;
-      src[j] = a.w + (size_t)(g < N ? g : N - 1) * K + k0 + chunk;
+      src[j] = a.w + (size_t)(g < N ? g : N - 1) * K + chunk;
       live[j] = true;
     } else {
       const uint32_t g = (uint32_t)(row - 16);
       live[j] = g < M;
-      src[j] = a.q + (size_t)(live[j] ? g : 0) * K + k0 + chunk;
+      src[j] = a.q + (size_t)(live[j] ? g : 0) * K + chunk;
     }
   }
   auto load = [&](uint32_t s) {
     int8_t* const base = ring + (s % R) * STAGE;
+    const size_t kc = S >= 8 ? (size_t)((s + blockIdx.x) % ST) * S + wave : (size_t)wave * ST + s;
 #pragma unroll
     for (int j = 0; j < L; ++j)
       if (live[j])
-        __builtin_amdgcn_global_load_lds((const void*)(src[j] + (size_t)s * 128),
+        __builtin_amdgcn_global_load_lds((const void*)(src[j] + kc * 128),
                                          W8A8_LDS_PTR(base + j * 1024 + lane * 16), 16, 0, 0);
   };
 
@@ -1112,7 +1120,8 @@ static bool split_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t& splits) {
 // 14.03) and keep it.  gate_up (24576 x 4096, 1,536 workgroups) measured
 // slower on it (M = 4 / 8 / 16 19.31 / 19.86 / 21.74 us against 18.23 /
 // 18.01 / 17.41 on the 96-column tiles).  Deeper rings (5) and 16 waves
-// measured level or slower.
+// measured level or slower.  These down figures are for contiguous K slices;
+// the interleaved order the kernel now takes at S = 8 runs 2-3% faster.
 static bool narrow_plan(uint32_t m, uint32_t n, uint32_t k, int& S, int& R, int& MB, int& LAL) {
   if (m == 0 || m > 32 || (n + 95) / 96 >= 224) return false;
   S = k >= 8192 ? 8 : 4;

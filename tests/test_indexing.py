@@ -82,13 +82,13 @@ def xcd_slot(b, G):
 
 
 def mfma32_rows_cols(lane, v):
-    """Row / column of value v of lane l in a 32 x 32 i32 MFMA block (gemm.hip:374-376)."""
+    """Row / column of value v of lane l in a 32 x 32 i32 MFMA block (gemm.hip:382-384)."""
     return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3), lane & 31
 
 
 def frag_offsets():
     """gemm_dma / gemm_tall fragment reads: lane l, sub-step i -> byte offset
-    inside a 32-row block of 128-byte LDS rows (gemm.hip:551-554, :821-824)."""
+    inside a 32-row block of 128-byte LDS rows (gemm.hip:559-562, :829-832)."""
     lane = np.arange(64)
     fr, fh = lane & 31, lane >> 5
     return np.stack([fr * 128 + (((2 * i + fh) ^ ((fr >> 1) & 7)) * 16) for i in range(4)])  # [4, 64]
@@ -98,7 +98,7 @@ def frag_offsets():
 def store_blocks(m, n, row0, col0, FM, FN):
     """(rows, cols) that store_blocks writes for wave tiles with top-left
     corners (row0, col0) (broadcast arrays), guarded by r < m, c < n
-    (gemm.hip:381-452).  Its epilogue loads are clamped (min(r, m - 1),
+    (gemm.hip:389-460).  Its epilogue loads are clamped (min(r, m - 1),
     min(c, n - 1)), hence always in bounds."""
     lane = np.arange(64)[:, None]
     v = np.arange(16)[None, :]
@@ -113,7 +113,7 @@ def store_blocks(m, n, row0, col0, FM, FN):
 
 
 def check_dma(m, n, k, r, residual):
-    """gemm_dma (gemm.hip:475-621) over its grid: DMA sources, LDS ring slots,
+    """gemm_dma (gemm.hip:483-629) over its grid: DMA sources, LDS ring slots,
     fragment reads, the stores of store_blocks."""
     BM, BN, WM, WN, SA, SB, splits = r["bm"], r["bn"], r["wm"], r["wn"], r["sa"], r["sb"], r["splits"]
     tm, tn = -(-m // BM), -(-n // BN)
@@ -164,7 +164,7 @@ def check_dma(m, n, k, r, residual):
 
 
 def check_tall(m, n, k, r, residual):
-    """gemm_tall (gemm.hip:738-937): per-wave DMA instruction dealing, the
+    """gemm_tall (gemm.hip:746-945): per-wave DMA instruction dealing, the
     rings, the two compute mappings, the stores."""
     BN, SA, SB, MA, splits = r["bn"], r["sa"], r["sb"], r["ma"], r["splits"]
     FN, ASL, BSL, NB = BN // 32, MA * 128, BN * 128, BN // 8
@@ -229,7 +229,7 @@ def check_tall(m, n, k, r, residual):
 
 
 def check_epilogue(m, n, r, residual):
-    """splitk_epilogue / splitk_epilogue8 (gemm.hip:952-1085): grid
+    """splitk_epilogue / splitk_epilogue8 (gemm.hip:960-1093): grid
     (ceil(n / cols / 256), min(m, 65535)), thread columns c .. c + cols - 1,
     rows blockIdx.y, + gridDim.y, ...; slab index clamped to splits - 1."""
     cols, splits = r["epi_cols"], r["splits"]
@@ -281,12 +281,15 @@ def check_skinny(m, n, k, r):
 
 
 def check_narrow(m, n, k, r):
-    """gemm_narrow (gemm.hip:268-372, plan :1116): grid ceil(n / 16) x 64 S
-    threads; wave w sums K slice [w K / S, (w + 1) K / S) in 128-byte stages
-    through its own R-stage ring; DMA instruction j < 2 + LAL fills rows
-    8j .. 8j + 7 of a stage (lane l: row 8j + l / 8, global chunk
-    (l % 8) ^ (row % 8)); rows 0-15 are weight rows n0 + row clamped to
-    n - 1, rows 16.. activation rows row - 16, loaded only below M."""
+    """gemm_narrow (gemm.hip:268-380, plan :1125): grid ceil(n / 16) x 64 S
+    threads; wave w sums ST = K / (128 S) of the 128-byte K chunks through
+    its own R-stage ring: at S = 4 stage s reads chunk w ST + s, at S = 8
+    chunk ((s + b) mod ST) S + w for workgroup b; the chunks of all waves
+    and stages of a workgroup must be every chunk of K exactly once.  DMA
+    instruction j < 2 + LAL fills rows 8j .. 8j + 7 of a stage (lane l: row
+    8j + l / 8, 16-byte piece (l % 8) ^ (row % 8)); rows 0-15 are weight
+    rows n0 + row clamped to n - 1, rows 16.. activation rows row - 16,
+    loaded only below M."""
     MB, S, LAL, R = r["mt"], r["s"], r["u"], r["sa"]
     assert r["grid_x"] == -(-n // 16) and r["grid_y"] == 1 and r["block"] == 64 * S and r["splits"] == 1
     assert k % (128 * S) == 0 and 16 * MB >= m
@@ -295,23 +298,35 @@ def check_narrow(m, n, k, r):
     ROWS, L = 16 * (1 + MB), 2 + LAL
     STAGE, RING = ROWS * 128, R * ROWS * 128
     assert L <= ROWS // 8 and S * RING <= 160 * 1024
-    KS = k // S
-    ST = KS // 128
+    ST = k // (128 * S)
     n0 = np.arange(r["grid_x"])[:, None] * 16
     lane = np.arange(64)
+    b = np.arange(r["grid_x"])
+
+    def kchunk(wave, st):
+        """K chunk of stage st of wave `wave`, per workgroup."""
+        if S >= 8:
+            return ((st + b) % ST) * S + wave
+        return np.full(b.shape, wave * ST + st)
+
+    seen = np.zeros((r["grid_x"], k // 128), np.int64)
+    for wave in range(S):
+        for st in range(ST):
+            np.add.at(seen, (b, kchunk(wave, st)), 1)
+    assert (seen == 1).all(), "every K chunk exactly once per workgroup"
     for wave in range(S):
         for st in ({0, ST - 1} if ST > 0 else set()):
             for j in range(L):
                 row = 8 * j + (lane >> 3)
                 chunk = ((lane & 7) ^ (row & 7)) * 16
-                koff = wave * KS + st * 128 + chunk
+                koff = kchunk(wave, st)[:, None] * 128 + chunk
                 if j < 2:
                     src = np.minimum(n0 + row, n - 1) * k + koff
                     within("gemm_narrow W", src, src + 16, n * k)
                 else:
                     g = row - 16
                     live = g < m
-                    src = (g * k + koff)[live]
+                    src = (g * k + koff)[:, live]
                     within("gemm_narrow A", src, src + 16, m * k)
                 dst = wave * RING + (st % R) * STAGE + j * 1024 + lane * 16
                 within("gemm_narrow LDS DMA", dst, dst + 16, S * RING)
