@@ -146,7 +146,7 @@ hipError_t launch_gemv_produce(hipStream_t st, const ProduceArgs& p);
 // a.q_out is set); without it maxima[0] is left as the norm reset it.
 hipError_t launch_gemv_swiglu_norm(hipStream_t st, const ProduceArgs& p, const SwigluArgs& a, bool row_tail);
 // The SwiGLU row tail folded into the M = 1, K = 12288 GEMV that consumes
-// its codes (gemv_m1_rowtail).
+// its codes (gemv_rowtail_split).
 struct RowtailArgs {
   const void* act;   // [12288], act_dtype (F32 or BF16)
   int act_dtype;
