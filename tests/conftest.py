@@ -122,3 +122,32 @@ def bf16_ulp_distance(a, b) -> np.ndarray:
     ia = (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.int64)
     ib = (np.ascontiguousarray(b, np.float32).view(np.uint32) >> 16).astype(np.int64)
     return np.abs(ia - ib)
+
+
+def seeded_linear_shapes(count: int = 48, seed: int = 20261202) -> list[tuple[int, int, int]]:
+    """Seeded (m, n, k) for the linear sweeps (GPU parity and the indexing
+    replay), three kinds in turn, at most 64 Mi weights and 2e9
+    multiply-adds each:
+      - m log-uniform in [1, 700], n in [1, 30000] (log-uniform);
+      - the same with n in [2000, 30000] (the wide tiles);
+      - m in [17, 256], n in [2000, 30000], k a multiple of 1024 (the
+        one-M-tile plans and their split-K routes).
+    Outside the third kind k is a multiple of 1024 (40%: the narrow
+    plans), of 128 (30%: the DMA routes) or of 16 (30%: the guarded
+    tiles), up to 12800."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        kind = len(out) % 3
+        if kind == 2:
+            m = int(np.exp(rng.uniform(np.log(17.0), np.log(257.0))))
+            k = 1024 * int(rng.integers(1, 13))
+        else:
+            m = int(np.exp(rng.uniform(0.0, np.log(700.0))))
+            u = rng.random()
+            k = (1024 * int(rng.integers(1, 13)) if u < 0.4 else 128 * int(rng.integers(1, 101)) if u < 0.7
+                 else 16 * int(rng.integers(1, 801)))
+        n = int(np.exp(rng.uniform(np.log(2000.0) if kind else 0.0, np.log(30000.0))))
+        if n * k <= 64 << 20 and m * n * k <= 2_000_000_000:
+            out.append((m, n, k))
+    return out

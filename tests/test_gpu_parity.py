@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import argmax_cases, argmax_expected, rounding_expected, rounding_probe_inputs
+from conftest import (argmax_cases, argmax_expected, rounding_expected, rounding_probe_inputs,
+                      seeded_linear_shapes)
 from inferrous_amd import (CudaContext, DeviceBuffer, Event, Graph, W8A8Error, cfg, load, rows)
 from inferrous_amd import synth
 
@@ -175,6 +176,39 @@ def test_linear_random_shapes(env, m):
             ob = DeviceBuffer.zeroed(s, m * n, np.uint16)
             getattr(mod, op)(s, None, dq, da, dw, dws, k, ob)
             assert np.array_equal(ob.to_host_vec(s), outb), f"{op} bf16 m={m} n={n} k={k}"
+
+
+@pytest.mark.parametrize("m,n,k", seeded_linear_shapes())
+def test_linear_seeded_shape_sweep(env, m, n, k):
+    """Every family -- AUTO with the module's split-K workspace, the dot4
+    GEMV forced and the MFMA family forced -- at seeded random shapes that
+    land on every route and its tails: i32 accumulators, BF16 outputs and,
+    through linear_residual, f32 outputs with the residual sum, each bit for
+    bit against the oracle."""
+    ctx, mod, s = env
+    print(f"sweep m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m * 1_000_003 + n * 101 + k)
+    q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    q[0] = 127
+    w[-1] = -127
+    asc = (rng.random(m) / 64).astype(F32)
+    ws = (rng.random(n) / 64).astype(F32)
+    res = rng.standard_normal(m * n).astype(F32)
+    acc, out, outb = oracle.linear(q, asc, w, ws, k)
+    comb_want = oracle.residual(res, out.reshape(-1))
+    dq, da, dw, dws, dres = dev(s, q), dev(s, asc), dev(s, w), dev(s, ws), dev(s, res)
+    for op in ("linear", "linear_dot4", "linear_mfma"):
+        o32 = DeviceBuffer.zeroed(s, m * n, np.int32)
+        getattr(mod, op)(s, None, dq, da, dw, dws, k, o32)
+        assert np.array_equal(o32.to_host_vec(s), acc.reshape(-1)), f"{op} acc m={m} n={n} k={k}"
+        ob = DeviceBuffer.zeroed(s, m * n, np.uint16)
+        getattr(mod, op)(s, None, dq, da, dw, dws, k, ob)
+        assert np.array_equal(ob.to_host_vec(s), outb.reshape(-1)), f"{op} bf16 m={m} n={n} k={k}"
+    of, cf = DeviceBuffer.zeroed(s, m * n, np.float32), DeviceBuffer.zeroed(s, m * n, np.float32)
+    mod.linear_residual(s, None, dq, da, dw, dws, k, dres, of, cf)
+    assert np.array_equal(bits(of.to_host_vec(s)), bits(out.reshape(-1))), f"residual out m={m} n={n} k={k}"
+    assert np.array_equal(bits(cf.to_host_vec(s)), bits(comb_want)), f"residual sum m={m} n={n} k={k}"
 
 
 @pytest.mark.parametrize("m", [7, 8, 12, 16, 17, 23, 24, 32, 33])

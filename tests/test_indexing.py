@@ -26,6 +26,7 @@ import ctypes
 import numpy as np
 import pytest
 
+from conftest import seeded_linear_shapes
 from inferrous_amd import _lib
 
 F32, BF16, I32 = 0, 1, 2  # W8A8_OUT_* (include/inferrous_w8a8.h)
@@ -561,6 +562,20 @@ def test_narrow_every_m(n, k):
                 assert r["family"] == 15, (m, n, k, r)
             took += r["family"] == 15
     assert took >= 16
+
+
+@pytest.mark.parametrize("m,n,k", seeded_linear_shapes())
+def test_seeded_shape_sweep(m, n, k):
+    """The shapes of the GPU sweep (test_gpu_parity.test_linear_seeded_shape_sweep),
+    replayed first here on every path it runs: AUTO with and without the
+    split-K workspace, BF16 and f32 with the residual; the dot4 GEMV and
+    the MFMA family forced."""
+    wsb = workspace_bytes(m, n, k)
+    for path in (AUTO, DOT4, MFMA):
+        for workspace in ((0, wsb) if path != DOT4 else (0,)):
+            check_linear(m, n, k, path=path, workspace=workspace)
+            check_linear(m, n, k, F32, residual=True, path=path, workspace=workspace)
+    check_linear(m, n, k, I32, path=MFMA, workspace=wsb)
 
 
 def test_every_family_is_replayed():
