@@ -761,7 +761,8 @@ def main() -> int:
                            DeviceBuffer.view_of(gw, ffn * 4096, ffn * 4096),
                            DeviceBuffer.view_of(gws, ffn, ffn)))
 
-        def layer_chain(fused_mlp: bool = False, fused_producers: bool = False):
+        def layer_chain(fused_mlp: bool = False, fused_producers: bool = False, mlp_bufs=None):
+            gb_, ub_, ab_ = mlp_bufs or (gbuf, ubuf, act)
             for mats, (wg_, sg_, wu_, su_) in zip(layers, halves):
                 (_, _, _, wqkv, sqkv), (_, _, _, wo, so), _, (_, _, _, wd, sd) = mats
                 if fused_producers:
@@ -777,8 +778,8 @@ def main() -> int:
                 if fused_producers:
                     # the MLP block in two launches: norm_quantize folded into
                     # the SwiGLU GEMV, the act row tail into the down GEMV
-                    mod.norm_quantize_mlp(s, None, xs[4096], gains[1], normed, q4, sc4, wg_, sg_, gbuf, wu_, su_,
-                                          ubuf, act, mx, wd, sd, outs["down"], resid, comb, q12, sc12)
+                    mod.norm_quantize_mlp(s, None, xs[4096], gains[1], normed, q4, sc4, wg_, sg_, gb_, wu_, su_,
+                                          ub_, ab_, mx, wd, sd, outs["down"], resid, comb, q12, sc12)
                     continue
                 mod.norm_quantize(s, None, xs[4096], gains[1], normed, q4, sc4, mx)
                 if fused_mlp:
@@ -823,6 +824,15 @@ def main() -> int:
                      "lm_head"}
         log(f"decode chain, fused producers: {ms * 1e3:.1f} us "
             f"({extras['decode_chain_fused_producers']['GB/s']} GB/s)")
+        # the same with BF16 gate / up / act buffers: act is bf(silu(g) u),
+        # a BF16 value, so the codes and every output are the same bits, and
+        # the down GEMV's producers read a 24 KiB act row instead of 48 KiB
+        bf_bufs = tuple(DeviceBuffer.zeroed(s, ffn, np.uint16) for _ in range(3))
+        ms = time_graph(capture(lambda: layer_chain(fused_mlp=True, fused_producers=True, mlp_bufs=bf_bufs)), 20)
+        extras["decode_chain_fused_producers_bf16_mlp"] = {
+            "ms": round(ms, 4), "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "launches": 4 * synth.LAYERS + 3, "gate_up_act_dtype": "bf16"}
+        log(f"decode chain, fused producers, BF16 gate/up/act: {ms * 1e3:.1f} us")
         # latency-bound producers at M = 1: per call in a graph of 100
         # stream-ordered calls (launch gap included)
         act12 = DeviceBuffer.from_host(s, synth.normal_rows(45, 1, ffn).reshape(-1))
