@@ -437,6 +437,21 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.stdout == ""
 
 
+def test_bench_reads_the_committed_traffic_profile():
+    """roofline.traffic comes from the committed FETCH_SIZE / WRITE_SIZE
+    summary of the gate_up GEMV: the bench parses it, and it is within 2%
+    above the launch's algorithmic bytes (N K + 4 N + K + 4 + 2 N)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench_mod", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    traffic = bench.measured_traffic()
+    algorithmic = bench.gemv_bytes(24576, 4096)
+    assert traffic is not None
+    assert algorithmic <= traffic <= 1.02 * algorithmic, (traffic, algorithmic)
+
+
 def _fake(n, dtype):
     """A DeviceBuffer-shaped object for host-side validation only: a fake
     aligned address that no call reaches, since the checks raise first."""
