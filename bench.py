@@ -138,12 +138,14 @@ def head_profile_run() -> int:
     return 0
 
 
-def prefill_profile_run() -> int:
+def prefill_profile_run(warm_seconds: float = 0.0) -> int:
     """Workload for a kernel-trace profile of the prefill GEMMs: 8 layers of
     distinct weights (1.5 GB, above the MALL), the four projections at
-    M = 512 and M = 129, three eager passes each (no graphs); then a 256 MiB
-    device copy three times, the calibration kernel of known traffic for
-    counter passes (reads and writes 256 MiB)."""
+    M = 512 and M = 129, three eager passes each (no graphs), each M's
+    passes preceded by eager passes for warm_seconds (the count is printed,
+    so that a summary can skip them); then a 256 MiB device copy three
+    times, the calibration kernel of known traffic for counter passes
+    (reads and writes 256 MiB)."""
     from inferrous_amd import CudaContext, DeviceBuffer, load, synth
     from inferrous_amd import _lib
     ctx = CudaContext(0)
@@ -167,11 +169,19 @@ def prefill_profile_run() -> int:
             mod.quantize(s, None, DeviceBuffer.from_host(s, x), k, q, sc)
             pq[k] = (q, sc)
         outs = {name: DeviceBuffer.zeroed(s, m * n, np.uint16) for (name, n, _) in synth.DECODE_SHAPES}
-        for _ in range(3):
+
+        def one_pass():
             for (name, n, k, w, ws) in mats:
                 mod.linear(s, None, pq[k][0], pq[k][1], w, ws, k, outs[name])
+        warm, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < warm_seconds:
+            one_pass()
+            s.synchronize()
+            warm += 1
+        for _ in range(3):
+            one_pass()
         s.synchronize()
-        print(f"prefill M={m} done", flush=True)
+        print(f"prefill M={m} done after {warm} warm passes", flush=True)
     src = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
     dst = DeviceBuffer.zeroed(s, 256 << 20, np.uint8)
     for _ in range(3):
@@ -492,6 +502,8 @@ def main() -> int:
                     help="run only the decode layer chain workload for a kernel-trace profile")
     ap.add_argument("--ragged-profile", action="store_true",
                     help="run only the ragged small-batch workload for a kernel-trace profile")
+    ap.add_argument("--warm-seconds", type=float, default=0.0,
+                    help="--prefill-profile: eager passes before each M's three profiled passes")
     ap.add_argument("--timeline", action="store_true",
                     help="run only the per-wave clock timeline of the decode GEMV launches")
     ap.add_argument("--gemm-timeline", action="store_true",
@@ -506,7 +518,7 @@ def main() -> int:
     if args.traffic:
         return traffic_run()
     if args.prefill_profile:
-        return prefill_profile_run()
+        return prefill_profile_run(args.warm_seconds)
     if args.head_profile:
         return head_profile_run()
     if args.ragged_profile:
