@@ -1224,7 +1224,10 @@ static void launch_epilogue(hipStream_t st, const GemmArgs& a, uint32_t splits, 
 // 10.3 -> 9.7 us, M = 100 qkv 14.4 -> 13.5, M = 129 qkv 15.6-15.8 -> 14.9,
 // o 13.5-13.9 -> 13.1, down 22.6-24.1 -> 22.0, M = 200 qkv 18.7 -> 17.7;
 // but M = 255 o 15.9-16.1 -> 17.1, and level on gemm_dma's split route at
-// M = 300 and 512.
+// M = 300 and 512.  Two columns per thread (256- or 512-thread workgroups)
+// and four with 1,024-thread workgroups measured level or slower from M = 24
+// to 200 (M = 129 o 12.28-12.44 against 12.24 us, down 21.6-21.8 against
+// 21.5).
 static bool wide_epilogue(const GemmArgs& a) {
   return a.m > 200 && a.n % 8 == 0 && aligned16(a.partials) && aligned16(a.out) &&
          (a.out_dtype == W8A8_OUT_I32 || aligned16(a.ws)) &&
